@@ -1,0 +1,67 @@
+"""ctypes binding of the C ABI declared in ``include/rcsa.h``.
+
+The shared library is built in-tree by ``cast_amd.build``.  There is no
+fallback: every operator raises if the library is missing or a call fails.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_void_p
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "_lib" / "librcsa.so"
+
+RCSA_OK = 0
+RCSA_BF16 = 0
+RCSA_F32 = 1
+RCSA_ORDER_INDEX = 0
+RCSA_ORDER_RANK = 1
+
+_P = c_void_p
+_I = c_int64
+
+# name -> argument types (return type is int status unless noted)
+SIGNATURES: dict[str, list] = {
+    "rcsa_pool_query": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
+    "rcsa_pool_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P],
+    "rcsa_block_scores": [_P, _P, _I, _I, _I, _I, _P, _P],
+    "rcsa_select_topk": [_P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _P, _I, _P, c_int, _P],
+    "rcsa_quantize_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
+                          _P, _P, _P],
+    "rcsa_sparse_attn_bf16": [_P, _P, _P, _P, c_float, _P, _P, _P, _P] + [_I] * 18
+                             + [_I] * 8 + [_P],
+    "rcsa_sparse_attn_int8": [_P, _P, _I, _P, _P, _I, _P, _P, c_float, _P, _P, _P, _P]
+                             + [_I] * 18 + [_I] * 8 + [_P],
+    "rcsa_pack_tokens": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
+    "rcsa_unpack_tokens": [_P, _I, _I, _I, _I, _P, _I, _P, _P],
+    "rcsa_status_string": [c_int],
+    "rcsa_abi_version": [],
+}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    """Load ``librcsa.so`` once and declare every entry point's signature."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"RCSA HIP library not built: {LIB_PATH} is missing "
+            "(run `python -m cast_amd.build`)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, argtypes in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = argtypes
+        fn.restype = ctypes.c_char_p if name == "rcsa_status_string" else c_int
+    _lib = lib
+    return lib
+
+
+def check(status: int, fn: str) -> None:
+    """Raise ``RuntimeError("<fn>: <reason>")`` for a non-zero status."""
+    if status != RCSA_OK:
+        reason = load().rcsa_status_string(status).decode()
+        raise RuntimeError(f"{fn}: {reason} (status {status})")

@@ -1,0 +1,353 @@
+"""Tensor-level wrappers over the RCSA C ABI.
+
+Each function validates shapes/dtypes/devices on the host, allocates its
+outputs from the torch caching allocator, and launches on the current torch
+stream.  No function reads device memory back to the host.
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import RCSA_BF16, RCSA_F32, RCSA_ORDER_INDEX, RCSA_ORDER_RANK, check
+
+__all__ = [
+    "pool_query", "pool_key", "block_scores", "select_topk", "quantize_key",
+    "sparse_attn_bf16", "sparse_attn_int8", "pack_tokens", "unpack_tokens",
+]
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_code(t: torch.Tensor, fn: str) -> int:
+    if t.dtype == torch.bfloat16:
+        return RCSA_BF16
+    if t.dtype == torch.float32:
+        return RCSA_F32
+    raise TypeError(f"{fn}: expected bfloat16 or float32, got {t.dtype}")
+
+
+def _require_cuda(fn: str, *tensors: Optional[torch.Tensor]) -> None:
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(f"{fn}: tensors must live on a HIP device, got {t.device}")
+
+
+def _valid_u8(valid: Optional[torch.Tensor], n: int, device, fn: str) -> Optional[torch.Tensor]:
+    if valid is None:
+        return None
+    v = valid.reshape(-1)
+    if v.numel() != n:
+        raise ValueError(f"{fn}: valid mask has {v.numel()} entries, expected {n}")
+    if v.dtype != torch.uint8:
+        v = v.to(torch.uint8)
+    return v.to(device).contiguous()
+
+
+def _bhld(x: torch.Tensor, block_size: int, fn: str) -> tuple[int, int, int, int, int]:
+    if x.ndim != 4:
+        raise ValueError(f"{fn}: expected [B, H, L, D], got {tuple(x.shape)}")
+    B, H, L, D = x.shape
+    if L % block_size:
+        raise ValueError(f"{fn}: length {L} is not a multiple of block_size {block_size}")
+    if x.stride(3) != 1:
+        raise ValueError(f"{fn}: last dimension must be contiguous")
+    return B, H, L, D, L // block_size
+
+
+def pool_query(q: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
+               quantize: bool = False):
+    """Masked mean-pool + L2-normalise query blocks, optionally fusing int8 quantisation.
+
+    Follows P/matrix_curvature_phase_frame_weave.py:5685-5700.  Returns
+    ``(qhat [B*H, NB, D] fp32, q_i8 [B, H, L, D] int8 | None, q_scale [B*H, NB] | None)``.
+    """
+    fn = "pool_query"
+    _require_cuda(fn, q)
+    code = _dtype_code(q, fn)
+    B, H, L, D, NB = _bhld(q, block_size, fn)
+    v = _valid_u8(valid, L, q.device, fn)
+    qhat = torch.empty(B * H, NB, D, device=q.device, dtype=torch.float32)
+    q_i8 = torch.empty(B, H, L, D, device=q.device, dtype=torch.int8) if quantize else None
+    q_scale = torch.empty(B * H, NB, device=q.device, dtype=torch.float32) if quantize else None
+    st = _lib.load().rcsa_pool_query(
+        q.data_ptr(), code, B, H, NB, block_size, D, q.stride(0), q.stride(1), q.stride(2),
+        _ptr(v), qhat.data_ptr(), _ptr(q_i8), _ptr(q_scale), _stream())
+    check(st, fn)
+    return qhat, q_i8, q_scale
+
+
+def pool_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
+             stats: bool = False):
+    """Masked mean-pool + L2-normalise key blocks (+ sum/min/max for the quantiser).
+
+    Returns ``(khat, ksum, kmin, kmax)``; the last three are None unless ``stats``.
+    """
+    fn = "pool_key"
+    _require_cuda(fn, k)
+    code = _dtype_code(k, fn)
+    B, H, L, D, NB = _bhld(k, block_size, fn)
+    v = _valid_u8(valid, L, k.device, fn)
+    khat = torch.empty(B * H, NB, D, device=k.device, dtype=torch.float32)
+    if stats:
+        ksum, kmin, kmax = (torch.empty(B * H, NB, D, device=k.device, dtype=torch.float32)
+                            for _ in range(3))
+    else:
+        ksum = kmin = kmax = None
+    st = _lib.load().rcsa_pool_key(
+        k.data_ptr(), code, B, H, NB, block_size, D, k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), khat.data_ptr(), _ptr(ksum), _ptr(kmin), _ptr(kmax), _stream())
+    check(st, fn)
+    return khat, ksum, kmin, kmax
+
+
+def block_scores(qhat: torch.Tensor, khat: torch.Tensor) -> torch.Tensor:
+    """``score[bh] = qhat[bh] @ khat[bh]^T`` (P/matrix_curvature_phase_frame_weave.py:5701)."""
+    fn = "block_scores"
+    _require_cuda(fn, qhat, khat)
+    if qhat.dtype != torch.float32 or khat.dtype != torch.float32:
+        raise TypeError(f"{fn}: pooled vectors must be float32")
+    if qhat.ndim != 3 or khat.ndim != 3 or qhat.shape[0] != khat.shape[0] \
+            or qhat.shape[2] != khat.shape[2]:
+        raise ValueError(f"{fn}: shapes {tuple(qhat.shape)} / {tuple(khat.shape)}")
+    qhat = qhat.contiguous()
+    khat = khat.contiguous()
+    nbh, nq, d = qhat.shape
+    nk = khat.shape[1]
+    score = torch.empty(nbh, nq, nk, device=qhat.device, dtype=torch.float32)
+    check(_lib.load().rcsa_block_scores(qhat.data_ptr(), khat.data_ptr(), nbh, nq, nk, d,
+                                        score.data_ptr(), _stream()), fn)
+    return score
+
+
+def _mask_u8(mask: Optional[torch.Tensor], nbh: int, nq: int, nk: int, device, fn: str):
+    """Return (uint8 mask, head stride) for a [NQ, NK] or [NBH, NQ, NK] mask."""
+    if mask is None:
+        return None, 0
+    m = mask.to(device=device, dtype=torch.uint8)
+    if m.shape == (nq, nk):
+        return m.contiguous(), 0
+    if m.shape == (nbh, nq, nk):
+        return m.contiguous(), nq * nk
+    raise ValueError(f"{fn}: mask shape {tuple(mask.shape)} is neither [{nq}, {nk}] "
+                     f"nor [{nbh}, {nq}, {nk}]")
+
+
+def select_topk(score: torch.Tensor, k, *, forced: Optional[torch.Tensor] = None,
+                allowed: Optional[torch.Tensor] = None, max_k: Optional[int] = None,
+                order: str = "index"):
+    """Fixed-budget top-k over key blocks for every (bh, query block) row.
+
+    Order of preference: forced, then score descending, then block index
+    ascending (the stable-argsort tie rule of
+    P/qk_uncertainty_tangent_attention.py:978-980).  ``k`` is an int, or an
+    int tensor of shape [NQ] (shared by heads) or [NBH, NQ].  Returns
+    ``(indices int32 [NBH, NQ, max_k], counts int32 [NBH, NQ])``; unused
+    slots hold -1.
+    """
+    fn = "select_topk"
+    _require_cuda(fn, score)
+    if score.dtype != torch.float32 or score.ndim != 3:
+        raise TypeError(f"{fn}: score must be float32 [NBH, NQ, NK]")
+    score = score.contiguous()
+    nbh, nq, nk = score.shape
+    if isinstance(k, int):
+        row_k, stride, k_fixed = None, 0, int(k)
+        kmax = int(k)
+    else:
+        kt = torch.as_tensor(k)
+        if kt.shape == (nq,):
+            stride = 0
+        elif kt.shape == (nbh, nq):
+            stride = nq
+        else:
+            raise ValueError(f"{fn}: k tensor shape {tuple(kt.shape)}")
+        if max_k is None:
+            kmax = int(kt.max().item())  # host read of the budget; pass max_k to avoid it
+        else:
+            kmax = int(max_k)
+        row_k = kt.to(device=score.device, dtype=torch.int32).contiguous()
+        k_fixed = 0
+    if max_k is None:
+        max_k = max(1, min(kmax, nk))
+    if order not in ("index", "rank"):
+        raise ValueError(f"{fn}: order must be 'index' or 'rank'")
+    fm, fstride = _mask_u8(forced, nbh, nq, nk, score.device, fn)
+    am, astride = _mask_u8(allowed, nbh, nq, nk, score.device, fn)
+    if fm is not None and am is not None and fstride != astride:
+        # the ABI shares one head stride between the masks: broadcast both
+        fm = fm.expand(nbh, nq, nk).contiguous() if fstride == 0 else fm
+        am = am.expand(nbh, nq, nk).contiguous() if astride == 0 else am
+        fstride = astride = nq * nk
+    mstride = fstride if fm is not None else astride
+    indices = torch.empty(nbh, nq, max_k, device=score.device, dtype=torch.int32)
+    counts = torch.empty(nbh, nq, device=score.device, dtype=torch.int32)
+    st = _lib.load().rcsa_select_topk(
+        score.data_ptr(), nbh, nq, nk, _ptr(row_k), stride, k_fixed, _ptr(fm), _ptr(am),
+        mstride, indices.data_ptr(), max_k, counts.data_ptr(),
+        RCSA_ORDER_RANK if order == "rank" else RCSA_ORDER_INDEX, _stream())
+    check(st, fn)
+    return indices, counts
+
+
+def quantize_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
+                 ksum: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor):
+    """Per-head mean-smoothed, per-block symmetric int8 keys.
+
+    Returns ``(k_i8 [B, H, L, D], k_scale [B*H, NB], kmean [B*H, D])``.
+    """
+    fn = "quantize_key"
+    _require_cuda(fn, k, ksum, kmin, kmax)
+    code = _dtype_code(k, fn)
+    B, H, L, D, NB = _bhld(k, block_size, fn)
+    for t in (ksum, kmin, kmax):
+        if t.shape != (B * H, NB, D) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{fn}: statistics must be contiguous float32 [{B * H}, {NB}, {D}]")
+    v = _valid_u8(valid, L, k.device, fn)
+    kmean = torch.empty(B * H, D, device=k.device, dtype=torch.float32)
+    k_i8 = torch.empty(B, H, L, D, device=k.device, dtype=torch.int8)
+    k_scale = torch.empty(B * H, NB, device=k.device, dtype=torch.float32)
+    st = _lib.load().rcsa_quantize_key(
+        k.data_ptr(), code, B, H, NB, block_size, D, k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(),
+        k_i8.data_ptr(), k_scale.data_ptr(), _stream())
+    check(st, fn)
+    return k_i8, k_scale, kmean
+
+
+def _attn_common(q, k, v, indices, counts, fn):
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if t.ndim != 4 or t.stride(3) != 1:
+            raise ValueError(f"{fn}: {name} must be [B, H, L, D] with contiguous last dim")
+    if indices.ndim != 4 or counts.ndim != 3:
+        raise ValueError(f"{fn}: indices must be [B, H, NQB, maxK], lens [B, H, NQB]")
+    if indices.dtype != torch.int32 or counts.dtype != torch.int32:
+        raise TypeError(f"{fn}: indices/lens must be int32")
+    if indices.stride(3) != 1:
+        raise ValueError(f"{fn}: indices last dim must be contiguous")
+
+
+def _expand_lists(indices, counts, B, H):
+    # the reference expands a [1, 1, N, K] layout over (B, H) (stride 0 views)
+    return indices.expand(B, H, -1, -1), counts.expand(B, H, -1)
+
+
+def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block_n=128,
+                     sm_scale=None, return_lse=False, out=None):
+    """bf16 block-sparse attention; the ``_attn_fwd_bsa_align`` contract.
+
+    q/k/v [B, H, L, D] bf16, indices int32 [B|1, H|1, NQB, maxK], counts
+    int32 [B|1, H|1, NQB], valid: per key token (K_LEN entries) or None.
+    """
+    fn = "sparse_attn_bf16"
+    _require_cuda(fn, q, k, v, indices, counts)
+    _attn_common(q, k, v, indices, counts, fn)
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise TypeError(f"{fn}: q/k/v must be bfloat16")
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
+        raise ValueError(f"{fn}: k/v shape mismatch")
+    indices, counts = _expand_lists(indices, counts, B, H)
+    kv = _valid_u8(valid, Lk, q.device, fn)
+    if out is None:
+        out = torch.empty_like(q, memory_format=torch.contiguous_format)
+    lse = torch.empty(B, H, Lq, device=q.device, dtype=torch.float32) if return_lse else None
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    st = _lib.load().rcsa_sparse_attn_bf16(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(kv), scale, _ptr(lse), out.data_ptr(),
+        indices.data_ptr(), counts.data_ptr(),
+        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+        v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
+        indices.stride(0), indices.stride(1), indices.stride(2),
+        counts.stride(0), counts.stride(1), counts.stride(2),
+        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], _stream())
+    check(st, fn)
+    return (out, lse) if return_lse else out
+
+
+def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=None, *,
+                     block_m=128, block_n=128, sm_scale=None, return_lse=False, out=None):
+    """int8-QK / bf16-PV block-sparse attention over quantiser outputs."""
+    fn = "sparse_attn_int8"
+    _require_cuda(fn, q_i8, q_scale, k_i8, k_scale, v, indices, counts)
+    _attn_common(q_i8, k_i8, v, indices, counts, fn)
+    if q_i8.dtype != torch.int8 or k_i8.dtype != torch.int8 or v.dtype != torch.bfloat16:
+        raise TypeError(f"{fn}: q/k must be int8 and v bfloat16")
+    B, H, Lq, D = q_i8.shape
+    Lk = k_i8.shape[2]
+    if k_i8.shape != (B, H, Lk, D) or v.shape[:2] != (B, H) or v.shape[3] != D \
+            or v.shape[2] < Lk:
+        raise ValueError(f"{fn}: k/v shape mismatch")
+    nqb = -(-Lq // block_m)
+    nkb = -(-Lk // block_n)
+    if q_scale.dtype != torch.float32 or k_scale.dtype != torch.float32:
+        raise TypeError(f"{fn}: scales must be float32")
+    q_scale = q_scale.reshape(B * H, -1).contiguous()
+    k_scale = k_scale.reshape(B * H, -1).contiguous()
+    if q_scale.shape[1] < nqb or k_scale.shape[1] < nkb:
+        raise ValueError(f"{fn}: need {nqb} query and {nkb} key scales per head")
+    indices, counts = _expand_lists(indices, counts, B, H)
+    kv = _valid_u8(valid, Lk, q_i8.device, fn)
+    if out is None:
+        out = torch.empty(B, H, Lq, D, device=q_i8.device, dtype=torch.bfloat16)
+    lse = torch.empty(B, H, Lq, device=q_i8.device, dtype=torch.float32) if return_lse else None
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
+    st = _lib.load().rcsa_sparse_attn_int8(
+        q_i8.data_ptr(), q_scale.data_ptr(), q_scale.shape[1], k_i8.data_ptr(),
+        k_scale.data_ptr(), k_scale.shape[1], v.data_ptr(), _ptr(kv), scale, _ptr(lse),
+        out.data_ptr(), indices.data_ptr(), counts.data_ptr(),
+        q_i8.stride(0), q_i8.stride(1), q_i8.stride(2),
+        k_i8.stride(0), k_i8.stride(1), k_i8.stride(2),
+        v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
+        indices.stride(0), indices.stride(1), indices.stride(2),
+        counts.stride(0), counts.stride(1), counts.stride(2),
+        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], _stream())
+    check(st, fn)
+    return (out, lse) if return_lse else out
+
+
+def pack_tokens(x: torch.Tensor, slot_token: torch.Tensor) -> torch.Tensor:
+    """Gather ``x [B, L, H, D]`` into packed ``[B, H, n_slots, D]`` bf16; slot -1 -> zeros.
+
+    Mirrors ``q[:, flat].transpose(1, 2).contiguous(); q_packed[:, :, ~mask] = 0``
+    (P/matrix_curvature_phase_frame_weave.py:5671-5684).
+    """
+    fn = "pack_tokens"
+    _require_cuda(fn, x)
+    code = _dtype_code(x, fn)
+    if x.ndim != 4 or x.stride(3) != 1:
+        raise ValueError(f"{fn}: x must be [B, L, H, D] with contiguous last dim")
+    B, L, H, D = x.shape
+    st_ = slot_token.to(device=x.device, dtype=torch.int64).contiguous()
+    n_slots = st_.numel()
+    out = torch.empty(B, H, n_slots, D, device=x.device, dtype=torch.bfloat16)
+    check(_lib.load().rcsa_pack_tokens(x.data_ptr(), code, B, L, H, D, x.stride(0),
+                                       x.stride(1), x.stride(2), st_.data_ptr(), n_slots,
+                                       out.data_ptr(), _stream()), fn)
+    return out
+
+
+def unpack_tokens(packed: torch.Tensor, token_slot: torch.Tensor) -> torch.Tensor:
+    """``out[b, t, h] = packed[b, h, token_slot[t]]`` (P/matrix_curvature_phase_frame_weave.py:6095)."""
+    fn = "unpack_tokens"
+    _require_cuda(fn, packed)
+    if packed.dtype != torch.bfloat16 or packed.ndim != 4:
+        raise TypeError(f"{fn}: packed must be bfloat16 [B, H, n_slots, D]")
+    packed = packed.contiguous()
+    B, H, n_slots, D = packed.shape
+    ts = token_slot.to(device=packed.device, dtype=torch.int64).contiguous()
+    L = ts.numel()
+    out = torch.empty(B, L, H, D, device=packed.device, dtype=torch.bfloat16)
+    check(_lib.load().rcsa_unpack_tokens(packed.data_ptr(), B, H, n_slots, D, ts.data_ptr(),
+                                         L, out.data_ptr(), _stream()), fn)
+    return out

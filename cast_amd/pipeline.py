@@ -1,0 +1,78 @@
+"""The RCSA layer call on one GPU: pool/score -> top-k -> quantise -> sparse attention.
+
+This is the compute of ``_compact_cwca_attention``
+(P/matrix_curvature_phase_frame_weave.py:5643-6095) between the packed
+gather and the unpack, with the reference's torch eager pooling/top-k and
+the external Triton kernel replaced by the HIP kernels of ``librcsa.so``.
+Every launch is stream-ordered; nothing is read back to the host.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import ops
+
+
+@dataclass
+class RCSAResult:
+    out: torch.Tensor                 # [B, H, Lq, D] bf16
+    indices: torch.Tensor             # [B, H, NQB, max_k] int32
+    counts: torch.Tensor              # [B, H, NQB] int32
+    score: torch.Tensor               # [B*H, NQB, NKB] fp32
+    qhat: torch.Tensor
+    khat: torch.Tensor
+    lse: Optional[torch.Tensor] = None
+    q_i8: Optional[torch.Tensor] = None
+    q_scale: Optional[torch.Tensor] = None
+    k_i8: Optional[torch.Tensor] = None
+    k_scale: Optional[torch.Tensor] = None
+    kmean: Optional[torch.Tensor] = None
+
+
+def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                   q_valid: Optional[torch.Tensor], k_valid: Optional[torch.Tensor], *,
+                   block_size: int, k_select, forced: Optional[torch.Tensor] = None,
+                   allowed: Optional[torch.Tensor] = None, int8: bool = True,
+                   max_k: Optional[int] = None, sm_scale: Optional[float] = None,
+                   return_lse: bool = False, order: str = "index") -> RCSAResult:
+    """One RCSA layer call over packed Q/K/V ``[B, H, NB*BS, D]`` (bf16 or fp32).
+
+    ``k_select`` is the per-row number of key blocks handed to attention
+    (history budget + forced blocks such as the current chunk); ``forced``
+    marks blocks that are always kept, ``allowed`` the causal permissions.
+    With ``int8`` QK^T runs on int8 MFMA over smoothed per-block quantised
+    Q/K; otherwise on bf16 MFMA.
+    """
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    bs = block_size
+    qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs, quantize=int8)
+    khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs, stats=int8)
+    score = ops.block_scores(qhat, khat)
+    indices, counts = ops.select_topk(score, k_select, forced=forced, allowed=allowed,
+                                      max_k=max_k, order=order)
+    nqb = Lq // bs
+    idx4 = indices.view(B, H, nqb, -1)
+    cnt3 = counts.view(B, H, nqb)
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    lse = None
+    if int8:
+        k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax)
+        res = ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v if v.dtype == torch.bfloat16
+                                   else v.to(torch.bfloat16), idx4, cnt3, k_valid,
+                                   block_m=bs, block_n=bs, sm_scale=scale,
+                                   return_lse=return_lse)
+    else:
+        k_i8 = k_scale = kmean = None
+        qb = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
+        kb = k if k.dtype == torch.bfloat16 else k.to(torch.bfloat16)
+        vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
+        res = ops.sparse_attn_bf16(qb, kb, vb, idx4, cnt3, k_valid, block_m=bs, block_n=bs,
+                                   sm_scale=scale, return_lse=return_lse)
+    out, lse = res if return_lse else (res, None)
+    return RCSAResult(out, idx4, cnt3, score, qhat, khat, lse, q_i8, q_scale, k_i8, k_scale,
+                      kmean)

@@ -1,0 +1,223 @@
+/*
+ * rcsa.h -- C ABI of the MI355X (gfx950) Reconstruction-Coupled Sparse
+ * Attention (RCSA) hot path.
+ *
+ * Every entry point takes raw device pointers, element counts and strides
+ * (in elements, int64), the HIP stream to launch on, and returns an int
+ * status (RCSA_OK == 0).  Nothing here allocates device memory: outputs and
+ * scratch are owned by the caller.  Nothing here synchronises the stream or
+ * reads device memory on the host, so every call is stream-ordered.
+ *
+ * Reference paths below are relative to the CAST repository, with
+ * P/ = src/interaction_accel/methods/proposed/.
+ *
+ * Tensor conventions (all row-major, last dimension contiguous):
+ *   packed Q/K/V    [B, H, L, D]   token-major inside a head; L = blocks * block_size
+ *   pooled vectors  [B*H, NB, D]   fp32
+ *   block scores    [B*H, NQB, NKB] fp32
+ *   block lists     [B, H, NQB, max_k] int32, lens [B, H, NQB] int32
+ */
+#ifndef RCSA_H_
+#define RCSA_H_
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes returned by every entry point. */
+enum {
+  RCSA_OK = 0,
+  RCSA_ERR_NULL = 1,     /* a required pointer is NULL */
+  RCSA_ERR_SHAPE = 2,    /* unsupported or inconsistent sizes */
+  RCSA_ERR_STRIDE = 3,   /* last dimension not contiguous / misaligned stride */
+  RCSA_ERR_DTYPE = 4,    /* unsupported element type code */
+  RCSA_ERR_LAUNCH = 5,   /* the HIP runtime rejected the launch */
+  RCSA_ERR_ALIGN = 6     /* a pointer is not 16-byte aligned */
+};
+
+/* Element type codes for inputs that may be bf16 or fp32. */
+enum { RCSA_BF16 = 0, RCSA_F32 = 1 };
+
+/* Selection output order. */
+enum {
+  RCSA_ORDER_INDEX = 0, /* ascending block index (what the attention kernel streams best) */
+  RCSA_ORDER_RANK = 1   /* descending rank: forced first, then score desc, index asc */
+};
+
+/* Human-readable text for a status code (static storage). */
+const char* rcsa_status_string(int status);
+
+/* ABI version: (major << 16) | minor. */
+int rcsa_abi_version(void);
+
+/*
+ * Pooled query blocks, optionally fused with the int8 query quantiser.
+ *
+ * Replaces the query half of the masked mean-pool + F.normalize at
+ * P/matrix_curvature_phase_frame_weave.py:5685-5700 (native form:
+ * P/qk_uncertainty_tangent_attention.py:1013-1022 over the tiling of
+ * P/reciprocal_joint_attention.py:64-103):
+ *   qhat[bh, b, :] = normalize(sum_{t valid} q[bh, b*bs + t, :] / max(n_valid, 1))
+ * with normalize(x) = x / max(||x||_2, 1e-12).
+ * valid: uint8 [n_blocks * block_size] shared by every head, or NULL (all valid).
+ * When q_i8 and q_scale are both non-NULL the same pass writes the int8
+ * query (no reference counterpart; see rcsa_quantize_key):
+ *   q_scale[bh, b] = absmax_{t valid, c}(q) / 127   (1 when the block is all zero)
+ *   q_i8[bh, b*bs + t, c] = clamp(rne(q / q_scale), -127, 127), 0 on invalid tokens.
+ * q is addressed as q[bh_outer * stride_b + bh_inner * stride_h + token * stride_t + c]
+ * with bh = bh_outer * n_heads + bh_inner.  head_dim in {64, 128}; block_size in {64, 128}.
+ */
+int rcsa_pool_query(const void* q, int dtype, int64_t batch, int64_t n_heads,
+                    int64_t n_blocks, int64_t block_size, int64_t head_dim,
+                    int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                    const uint8_t* valid, float* qhat, int8_t* q_i8,
+                    float* q_scale, hipStream_t stream);
+
+/*
+ * Pooled key blocks plus the per-block statistics the key quantiser needs.
+ * Same pooling as rcsa_pool_query (the key half of
+ * P/matrix_curvature_phase_frame_weave.py:5685-5700).  Optional outputs
+ * (each [B*H, n_blocks, head_dim] fp32, all or none):
+ *   ksum = sum over valid tokens, kmin/kmax = min/max over valid tokens
+ *   (0 for blocks with no valid token).
+ */
+int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
+                  int64_t n_blocks, int64_t block_size, int64_t head_dim,
+                  int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                  const uint8_t* valid, float* khat, float* ksum, float* kmin,
+                  float* kmax, hipStream_t stream);
+
+/*
+ * Cosine block scores score[bh, i, j] = <qhat[bh, i], khat[bh, j]>.
+ * Replaces torch.matmul(q_content, k_content.transpose(-2, -1)) at
+ * P/matrix_curvature_phase_frame_weave.py:5701 and
+ * P/qk_uncertainty_tangent_attention.py:1023.
+ */
+int rcsa_block_scores(const float* qhat, const float* khat, int64_t n_bh,
+                      int64_t n_qblocks, int64_t n_kblocks, int64_t head_dim,
+                      float* score, hipStream_t stream);
+
+/*
+ * Fixed-budget top-k block selection, one wavefront per (bh, query block).
+ * Replaces score + 1e6 * local followed by torch.topk
+ * (P/matrix_curvature_phase_frame_weave.py:5829-5832) and the native stable
+ * descending argsort (P/qk_uncertainty_tangent_attention.py:970-980, 1025-1044).
+ * Total order: forced columns first, then higher score, then lower index.
+ * Only allowed columns are eligible; counts[row] = min(k_row, n_allowed).
+ *   row_k:   int32 k per row, element [bh * row_k_stride_bh + i]; NULL -> k_fixed
+ *   forced:  uint8 [NQB, NKB] (+ bh * mask_stride_bh) or NULL (none forced)
+ *   allowed: uint8 [NQB, NKB] (+ bh * mask_stride_bh) or NULL (all allowed)
+ *   indices: int32 [n_bh, NQB, max_k] (row stride max_k); slots >= count hold -1
+ *   counts:  int32 [n_bh, NQB]
+ * k values above max_k are clamped to max_k.  n_kblocks <= 65536.
+ */
+int rcsa_select_topk(const float* score, int64_t n_bh, int64_t n_qblocks,
+                     int64_t n_kblocks, const int32_t* row_k,
+                     int64_t row_k_stride_bh, int64_t k_fixed,
+                     const uint8_t* forced, const uint8_t* allowed,
+                     int64_t mask_stride_bh, int32_t* indices, int64_t max_k,
+                     int32_t* counts, int order, hipStream_t stream);
+
+/*
+ * int8 key quantiser with per-head mean smoothing.  No reference
+ * counterpart: the reference feeds bf16 keys to the sparse kernel
+ * (P/matrix_jit_spatial_acceleration.py:676-678).  Uses the statistics of
+ * rcsa_pool_key:
+ *   kmean[bh, c]    = sum_b ksum[bh, b, c] / max(sum_b n_valid(b), 1)
+ *   k_scale[bh, b]  = max_c max(kmax - kmean, kmean - kmin) / 127   (1 if 0)
+ *   k_i8[bh, t, c]  = clamp(rne((k - kmean) / k_scale), -127, 127), 0 on invalid tokens
+ * Softmax is invariant to the per-row constant q . kmean, so attention over
+ * the smoothed keys equals attention over the original keys.
+ */
+int rcsa_quantize_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
+                      int64_t n_blocks, int64_t block_size, int64_t head_dim,
+                      int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                      const uint8_t* valid, const float* ksum,
+                      const float* kmin, const float* kmax, float* kmean,
+                      int8_t* k_i8, float* k_scale, hipStream_t stream);
+
+/*
+ * Block-sparse flash attention, bf16 Q/K/V, fp32 online softmax.
+ * Drop-in for wan.modules.longcat_kernel._attn_fwd_bsa_align as launched by
+ * _longcat_active (P/matrix_jit_spatial_acceleration.py:663-729) and
+ * _longcat_asymmetric (P/matrix_curvature_phase_frame_weave.py:8847-8917):
+ * same argument meaning and order.  For every (b, h, query block m):
+ *   out[b,h,i,:] = softmax_j(sm_scale * q_i . k_j) v_j over the key tokens j of
+ *   blocks block_indices[b,h,m,0:lens[b,h,m]] with j < K_LEN and K_valid[j] != 0.
+ * M (nullable) receives the natural-log log-sum-exp of each row
+ * (-inf for a row with no admissible key, whose output row is 0).
+ * Indices outside [0, ceil(K_LEN/BLOCK_N)) are skipped; lens are clamped to
+ * [0, max_k].  Strides are in elements; every *_k / *_bs stride must be 1.
+ * HEAD_DIM in {64, 128}; BLOCK_M, BLOCK_N in {64, 128}.
+ */
+int rcsa_sparse_attn_bf16(const void* Q, const void* K, const void* V,
+                          const uint8_t* K_valid, float sm_scale, float* M,
+                          void* Out, const int32_t* block_indices,
+                          const int32_t* block_indices_lens,
+                          int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                          int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+                          int64_t stride_vz, int64_t stride_vh, int64_t stride_vn,
+                          int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                          int64_t stride_bz, int64_t stride_bh, int64_t stride_bm,
+                          int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                          int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
+                          int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
+                          int64_t max_k, hipStream_t stream);
+
+/*
+ * Block-sparse flash attention with int8 QK^T (i32 MFMA accumulate) and
+ * bf16 PV (fp32 MFMA accumulate), fp32 online softmax.  Same contract as
+ * rcsa_sparse_attn_bf16 with Q/K replaced by the quantiser outputs:
+ *   logits = sm_scale * q_scale[b*H+h, m] * k_scale[b*H+h, n] * (q_i8 . k_i8)
+ * q_scale has ceil(Q_LEN/BLOCK_M) entries per head and k_scale
+ * ceil(K_LEN/BLOCK_N) entries per head (row strides given).
+ */
+int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
+                          int64_t q_scale_stride, const int8_t* K,
+                          const float* k_scale, int64_t k_scale_stride,
+                          const void* V, const uint8_t* K_valid, float sm_scale,
+                          float* M, void* Out, const int32_t* block_indices,
+                          const int32_t* block_indices_lens,
+                          int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                          int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+                          int64_t stride_vz, int64_t stride_vh, int64_t stride_vn,
+                          int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                          int64_t stride_bz, int64_t stride_bh, int64_t stride_bm,
+                          int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                          int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
+                          int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
+                          int64_t max_k, hipStream_t stream);
+
+/*
+ * Gather compact tokens into the packed head-major layout, zeroing invalid
+ * slots.  Replaces q[:, flat].transpose(1, 2).contiguous(); q_packed[:, :, ~mask] = 0
+ * at P/matrix_curvature_phase_frame_weave.py:5671-5684.
+ *   x:      [B, L, H, D]   (strides in elements, last dim contiguous), bf16 or fp32
+ *   slot_token: int64 [n_slots]  source token of each packed slot, -1 = invalid
+ *   out:    [B, H, n_slots, D] bf16 (contiguous)
+ */
+int rcsa_pack_tokens(const void* x, int dtype, int64_t B, int64_t L, int64_t H,
+                     int64_t D, int64_t stride_b, int64_t stride_l,
+                     int64_t stride_h, const int64_t* slot_token,
+                     int64_t n_slots, void* out, hipStream_t stream);
+
+/*
+ * Scatter the packed attention output back to token order.  Replaces
+ * output_packed[:, token_to_packed] (P/matrix_curvature_phase_frame_weave.py:6095)
+ * after the .transpose(1, 2) of :6086-6094.
+ *   packed: [B, H, n_slots, D] bf16 (contiguous)
+ *   token_slot: int64 [L]  packed slot of each output token
+ *   out:    [B, L, H, D] bf16 (contiguous)
+ */
+int rcsa_unpack_tokens(const void* packed, int64_t B, int64_t H, int64_t n_slots,
+                       int64_t D, const int64_t* token_slot, int64_t L, void* out,
+                       hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RCSA_H_ */

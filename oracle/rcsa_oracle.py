@@ -1,0 +1,422 @@
+"""CPU oracle for the RCSA hot path -- TEST INFRASTRUCTURE ONLY.
+
+This module is the checker.  Only ``tests/``, ``__graft_entry__.smoke()`` and
+the ``cpu_baseline`` leg of ``bench.py`` may import it; the product path in
+``cast_amd`` never does.  It restates, in plain PyTorch eager on the CPU
+(fp32, fp64 where noted), what the CAST reference computes on this path.
+Paths are relative to the CAST repository, P/ =
+src/interaction_accel/methods/proposed/.
+
+How each function is pinned (beyond being a restatement) is listed in its
+docstring; the pins live in tests/test_oracle_pins.py:
+  pool_blocks         fp64 brute-force loops; constant-block and zero-block closed forms
+  block_scores        fp64 loops; Cauchy-Schwarz bound |s| <= 1; s(x, x) = 1
+  local_stencil       pure-Python Manhattan loop
+  select_topk         brute-force Python sort with tuple keys; forced/allowed invariants
+  topk_margin         brute-force sort
+  quantize_*          dequantisation error <= scale / 2; range [-127, 127]; idempotence
+  sparse_attention    fp64 per-row loops; single-key => v; equal logits => mean(v);
+                      per-row shift invariance of softmax
+  compact_layout      reference's loop branch restated with pure-Python lists
+  apportion*          exact rational arithmetic (fractions.Fraction) + conserved sums
+"""
+from __future__ import annotations
+
+import math
+from typing import Optional, Sequence
+
+import torch
+import torch.nn.functional as F
+
+__all__ = [
+    "pool_blocks", "block_scores", "local_stencil", "select_topk", "topk_margin",
+    "quantize_query_blocks", "key_mean", "quantize_key_blocks", "dequantize_blocks",
+    "sparse_attention", "sparse_attention_int8", "equivalence_stats", "compact_layout",
+    "apportion", "apportion_section_matrix", "budget_blocks", "rcsa_layer",
+]
+
+
+# --------------------------------------------------------------------------
+# a2 / a3: pooling and cosine scores
+
+def pool_blocks(x: torch.Tensor, valid: Optional[torch.Tensor], block_size: int):
+    """Masked mean over each block's valid tokens, then F.normalize.
+
+    Restates P/matrix_curvature_phase_frame_weave.py:5685-5700
+    (weights = valid, denominator = weights.sum().clamp_min(1)).
+    x: [B, H, NB*BS, D]; valid: [NB*BS] bool/uint8 or None.
+    Returns (hat [B, H, NB, D] fp32, block sums [B, H, NB, D] fp32, n_valid [NB]).
+    """
+    B, H, L, D = x.shape
+    nb = L // block_size
+    xb = x.reshape(B, H, nb, block_size, D).float()
+    if valid is None:
+        w = torch.ones(nb, block_size)
+    else:
+        w = valid.reshape(nb, block_size).float()
+    weights = w[None, None, :, :, None]
+    sums = (xb * weights).sum(dim=3)
+    denom = weights.sum(dim=3).clamp_min(1.0)
+    hat = F.normalize(sums / denom, dim=-1)
+    return hat, sums, w.sum(dim=1)
+
+
+def block_scores(qhat: torch.Tensor, khat: torch.Tensor) -> torch.Tensor:
+    """score = q_content @ k_content^T (P/matrix_curvature_phase_frame_weave.py:5701)."""
+    return torch.matmul(qhat, khat.transpose(-2, -1))
+
+
+def local_stencil(n_blocks: int, nh: int, nw: int) -> torch.Tensor:
+    """Manhattan <= 1 neighbourhood in (t, h, w) block coordinates.
+
+    Restates P/matrix_curvature_phase_frame_weave.py:5718-5725 and
+    P/qk_uncertainty_tangent_attention.py:1025-1039 (block id = t*nh*nw + h*nw + w).
+    """
+    spatial = nh * nw
+    ids = torch.arange(n_blocks)
+    bt, rem = ids // spatial, ids % spatial
+    bh, bw = rem // nw, rem % nw
+    return ((bt[:, None] - bt[None, :]).abs() + (bh[:, None] - bh[None, :]).abs()
+            + (bw[:, None] - bw[None, :]).abs()) <= 1
+
+
+# --------------------------------------------------------------------------
+# a4 / a6: forced set and top-k
+
+def _broadcast_mask(mask, nbh, nq, nk, default):
+    if mask is None:
+        return torch.full((nbh, nq, nk), default, dtype=torch.bool)
+    m = mask.bool()
+    if m.shape == (nq, nk):
+        m = m[None].expand(nbh, nq, nk)
+    return m
+
+
+def _row_k(k, nbh, nq):
+    if isinstance(k, int):
+        return torch.full((nbh, nq), k, dtype=torch.int64)
+    kt = torch.as_tensor(k).to(torch.int64)
+    if kt.shape == (nq,):
+        kt = kt[None].expand(nbh, nq)
+    return kt
+
+
+def select_topk(score: torch.Tensor, k, *, forced=None, allowed=None,
+                max_k: Optional[int] = None, order: str = "index"):
+    """Top-k per (bh, query block) under the total order
+    (allowed, forced, score desc, index asc).
+
+    Restates ``torch.topk(score + 1e6 * local, k)`` at
+    P/matrix_curvature_phase_frame_weave.py:5829-5831 with forced blocks as a
+    mask instead of +1e6 (fp32 has a 0.0625 ulp at 1e6), and the stable
+    descending argsort of P/qk_uncertainty_tangent_attention.py:978-980 for
+    ties (lower index first).  Disallowed columns (the -inf topology mask of
+    P/qk_uncertainty_tangent_attention.py:820) are never selected.
+    score: [NBH, NQ, NK].  Returns (indices int32 [NBH, NQ, max_k] padded
+    with -1, counts int32 [NBH, NQ]).
+    """
+    nbh, nq, nk = score.shape
+    fm = _broadcast_mask(forced, nbh, nq, nk, False)
+    am = _broadcast_mask(allowed, nbh, nq, nk, True)
+    kk = _row_k(k, nbh, nq)
+    if max_k is None:
+        max_k = max(1, min(int(kk.max()), nk))
+    kk = kk.clamp(0, max_k)
+    s = score.float().clone()
+    s[s == 0] = 0.0  # -0 == +0
+    s = torch.where(torch.isnan(s), torch.full_like(s, float("inf")), s)
+    # stable sorts from the least significant key to the most significant
+    idx = torch.arange(nk).expand(nbh, nq, nk)
+    order1 = torch.sort(s, dim=-1, descending=True, stable=True).indices
+    f1 = torch.gather(fm, -1, order1)
+    order2 = torch.gather(order1, -1, torch.sort(f1.to(torch.int8), dim=-1,
+                                                 descending=True, stable=True).indices)
+    a2 = torch.gather(am, -1, order2)
+    order3 = torch.gather(order2, -1, torch.sort(a2.to(torch.int8), dim=-1,
+                                                 descending=True, stable=True).indices)
+    n_allowed = am.sum(-1)
+    counts = torch.minimum(kk, n_allowed).to(torch.int32)
+    out = torch.full((nbh, nq, max_k), -1, dtype=torch.int32)
+    for r in range(nbh):
+        for i in range(nq):
+            c = int(counts[r, i])
+            sel = order3[r, i, :c]
+            if order == "index":
+                sel = torch.sort(sel).values
+            out[r, i, :c] = sel.to(torch.int32)
+    del idx
+    return out, counts
+
+
+def topk_margin(score: torch.Tensor, k, *, forced=None, allowed=None) -> torch.Tensor:
+    """Score gap between the last selected and the first rejected column.
+
+    inf when the boundary separates a forced from a non-forced column or when
+    every allowed column is selected.  [NBH, NQ] fp32.
+    """
+    nbh, nq, nk = score.shape
+    fm = _broadcast_mask(forced, nbh, nq, nk, False)
+    am = _broadcast_mask(allowed, nbh, nq, nk, True)
+    kk = _row_k(k, nbh, nq)
+    out = torch.full((nbh, nq), float("inf"))
+    for r in range(nbh):
+        for i in range(nq):
+            cols = [(bool(fm[r, i, j]), float(score[r, i, j]), j)
+                    for j in range(nk) if am[r, i, j]]
+            cols.sort(key=lambda t: (not t[0], -t[1], t[2]))
+            c = min(int(kk[r, i]), len(cols))
+            if 0 < c < len(cols) and cols[c - 1][0] == cols[c][0]:
+                out[r, i] = cols[c - 1][1] - cols[c][1]
+    return out
+
+
+# --------------------------------------------------------------------------
+# a10: int8 Q/K quantiser (no reference counterpart)
+
+def quantize_query_blocks(q: torch.Tensor, valid, block_size: int):
+    """Per (head, block) symmetric int8: scale = absmax/127, q8 = rne(q * (127/absmax)).
+
+    Returns (q_i8 [B,H,L,D] int8, scale [B*H, NB] fp32).  Invalid tokens -> 0.
+    """
+    B, H, L, D = q.shape
+    nb = L // block_size
+    x = q.float().reshape(B, H, nb, block_size, D)
+    w = (torch.ones(nb, block_size, dtype=torch.bool) if valid is None
+         else valid.reshape(nb, block_size).bool())
+    wm = w[None, None, :, :, None]
+    amax = torch.where(wm, x.abs(), torch.zeros_like(x)).amax(dim=(3, 4))
+    live = amax > 0
+    scale = torch.where(live, amax / 127.0, torch.ones_like(amax))
+    inv = torch.where(live, torch.tensor(127.0) / amax, torch.ones_like(amax))
+    q8 = torch.round(x * inv[..., None, None]).clamp(-127, 127)
+    q8 = torch.where(wm, q8, torch.zeros_like(q8)).to(torch.int8)
+    return q8.reshape(B, H, L, D), scale.reshape(B * H, nb)
+
+
+def key_mean(k: torch.Tensor, valid) -> torch.Tensor:
+    """Per-head, per-channel mean over all valid key tokens (fp64 accumulate). [B*H, D]."""
+    B, H, L, D = k.shape
+    w = torch.ones(L, dtype=torch.bool) if valid is None else valid.reshape(L).bool()
+    x = k.double() * w[None, None, :, None]
+    return (x.sum(dim=2) / max(int(w.sum()), 1)).float().reshape(B * H, D)
+
+
+def quantize_key_blocks(k: torch.Tensor, valid, block_size: int, kmean: torch.Tensor):
+    """Mean-smoothed per-block symmetric int8 keys given the per-head mean.
+
+    scale = max |k - m| / 127 over the block's valid tokens; k8 = rne((k - m) * (127/amax)).
+    Returns (k_i8 [B,H,L,D], scale [B*H, NB]).
+    """
+    B, H, L, D = k.shape
+    nb = L // block_size
+    m = kmean.reshape(B, H, 1, 1, D).float()
+    x = k.float().reshape(B, H, nb, block_size, D) - m
+    w = (torch.ones(nb, block_size, dtype=torch.bool) if valid is None
+         else valid.reshape(nb, block_size).bool())
+    wm = w[None, None, :, :, None]
+    amax = torch.where(wm, x.abs(), torch.zeros_like(x)).amax(dim=(3, 4))
+    live = (amax > 0) & w.any(dim=1)[None, None]
+    scale = torch.where(live, amax / 127.0, torch.ones_like(amax))
+    inv = torch.where(live, torch.tensor(127.0) / amax, torch.ones_like(amax))
+    k8 = torch.round(x * inv[..., None, None]).clamp(-127, 127)
+    k8 = torch.where(wm, k8, torch.zeros_like(k8)).to(torch.int8)
+    return k8.reshape(B, H, L, D), scale.reshape(B * H, nb)
+
+
+def dequantize_blocks(x_i8: torch.Tensor, scale: torch.Tensor, block_size: int):
+    """x_i8 * scale broadcast per block -> fp32 [B, H, L, D]."""
+    B, H, L, D = x_i8.shape
+    nb = L // block_size
+    s = scale.reshape(B, H, nb, 1, 1)
+    return (x_i8.float().reshape(B, H, nb, block_size, D) * s).reshape(B, H, L, D)
+
+
+# --------------------------------------------------------------------------
+# a8: block-sparse attention
+
+def sparse_attention(q, k, v, indices, counts, kvalid=None, *, block_m: int, block_n: int,
+                     sm_scale: Optional[float] = None, dtype=torch.float32,
+                     heads: Optional[Sequence[int]] = None,
+                     qblocks: Optional[Sequence[int]] = None):
+    """Explicit softmax over the allowed key tokens of each query block.
+
+    Restates the reference's own oracle at
+    P/matrix_jit_spatial_acceleration.py:836-858 (logits = q.k / sqrt(D),
+    softmax over the listed blocks' valid keys, weights @ v) for every query
+    row, which is the contract of _attn_fwd_bsa_align as launched at :663-729.
+    Rows with no admissible key get 0 output and lse = -inf.
+    q: [B,H,Lq,D], k/v: [B,H,Lk,D], indices [B|1,H|1,NQB,maxK], counts [B|1,H|1,NQB].
+    Optional ``heads``/``qblocks`` restrict the work (other rows left 0).
+    Returns (out [B,H,Lq,D] dtype, lse [B,H,Lq] dtype).
+    """
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    nqb = -(-Lq // block_m)
+    nkb = -(-Lk // block_n)
+    indices = indices.expand(B, H, -1, -1)
+    counts = counts.expand(B, H, -1)
+    kv = (torch.ones(Lk, dtype=torch.bool) if kvalid is None
+          else kvalid.reshape(-1).bool())
+    out = torch.zeros(B, H, Lq, D, dtype=dtype)
+    lse = torch.full((B, H, Lq), float("-inf"), dtype=dtype)
+    hs = range(H) if heads is None else heads
+    qbs = range(nqb) if qblocks is None else qblocks
+    maxk = indices.shape[-1]
+    for b in range(B):
+        for h in hs:
+            for m in qbs:
+                c = max(0, min(int(counts[b, h, m]), maxk))
+                blocks = [int(n) for n in indices[b, h, m, :c] if 0 <= int(n) < nkb]
+                toks = [t for n in blocks for t in range(n * block_n, min((n + 1) * block_n, Lk))]
+                toks = torch.tensor(toks, dtype=torch.long)
+                if toks.numel():
+                    toks = toks[kv[toks]]
+                r0, r1 = m * block_m, min((m + 1) * block_m, Lq)
+                if toks.numel() == 0:
+                    continue
+                qq = q[b, h, r0:r1].to(dtype)
+                kk = k[b, h, toks].to(dtype)
+                vv = v[b, h, toks].to(dtype)
+                logits = (qq @ kk.T) * scale
+                out[b, h, r0:r1] = torch.softmax(logits, dim=-1) @ vv
+                lse[b, h, r0:r1] = torch.logsumexp(logits, dim=-1)
+    return out, lse
+
+
+def sparse_attention_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, kvalid=None, *,
+                          block_m: int, block_n: int, sm_scale: Optional[float] = None,
+                          heads=None, qblocks=None):
+    """fp32 attention over the dequantised int8 Q/K (what the int8 kernel computes
+    before its bf16 rounding of P), same contract as :func:`sparse_attention`."""
+    q = dequantize_blocks(q_i8, q_scale, block_m)
+    k = dequantize_blocks(k_i8, k_scale, block_n)
+    return sparse_attention(q, k, v.float(), indices, counts, kvalid, block_m=block_m,
+                            block_n=block_n, sm_scale=sm_scale, heads=heads, qblocks=qblocks)
+
+
+def equivalence_stats(reference: torch.Tensor, candidate: torch.Tensor) -> dict:
+    """relative_l2 / cosine / mae / max_abs, as P/matrix_jit_spatial_acceleration.py:880-897."""
+    r = reference.detach().float()
+    c = candidate.detach().float()
+    d = c - r
+    return {
+        "relative_l2": float(torch.linalg.vector_norm(d) / (torch.linalg.vector_norm(r) + 1e-12)),
+        "cosine": float(F.cosine_similarity(r.reshape(-1), c.reshape(-1), dim=0)),
+        "mae": float(d.abs().mean()),
+        "max_abs": float(d.abs().max()),
+    }
+
+
+# --------------------------------------------------------------------------
+# a1: compact packed-block layout
+
+def compact_layout(active_frames: Sequence[int], memory_temporal: int, height: int,
+                   width: int, block_shape: tuple[int, int, int]):
+    """Packed 128-slot block map of the compact active frames.
+
+    Restates P/matrix_curvature_phase_frame_weave.py:5223-5301 through its
+    per-block loop branch (:5290-5293): block members are the compact tokens
+    with that block id, in increasing token order.
+    Returns (block_indices [NB, BS] int64 with -1 padding, valid [NB, BS] bool,
+    token_to_packed [T*H*W] int64).
+    """
+    tt, th, tw = block_shape
+    frames = sorted(int(f) for f in active_frames)
+    compact_t = len(frames)
+    spatial = height * width
+    nh, nw = -(-height // th), -(-width // tw)
+    compact_memory = sum(1 for f in frames if f < memory_temporal)
+    if compact_memory:
+        memory_cells = -(-compact_memory // tt)
+        n_blocks = (memory_cells + -(-(compact_t - compact_memory) // tt)) * nh * nw
+    else:
+        memory_cells = 0
+        n_blocks = -(-compact_t // tt) * nh * nw
+    block_size = tt * th * tw
+    members: list[list[int]] = [[] for _ in range(n_blocks)]
+    for tok in range(compact_t * spatial):
+        lt, ls = tok // spatial, tok % spatial
+        lh, lw = ls // width, ls % width
+        if compact_memory:
+            cell = lt // tt if lt < compact_memory else memory_cells + (lt - compact_memory) // tt
+        else:
+            cell = lt // tt
+        members[cell * nh * nw + (lh // th) * nw + lw // tw].append(tok)
+    idx = torch.full((n_blocks, block_size), -1, dtype=torch.long)
+    t2p = torch.empty(compact_t * spatial, dtype=torch.long)
+    for b, mem in enumerate(members):
+        if len(mem) > block_size:
+            raise RuntimeError("compact frame block exceeds its packed capacity")
+        for slot, tok in enumerate(mem):
+            idx[b, slot] = tok
+            t2p[tok] = b * block_size + slot
+    return idx, idx >= 0, t2p
+
+
+# --------------------------------------------------------------------------
+# a5: budgets
+
+def apportion(weights: Sequence[float], total: int) -> list[int]:
+    """Largest-remainder apportionment, ties to the lower index.
+
+    Restates P/qk_uncertainty_tangent_attention.py:847-865 with exact
+    rational arithmetic (the reference uses fp32; equal unless a fractional
+    part differs by < 1 ulp).
+    """
+    from fractions import Fraction
+    w = [max(Fraction(x), Fraction(0)) for x in weights]
+    if sum(w) <= 0:
+        w = [Fraction(1)] * len(w)
+    tot = sum(w)
+    raw = [Fraction(total) * x / tot for x in w]
+    res = [math.floor(r) for r in raw]
+    rem = total - sum(res)
+    order = sorted(range(len(w)), key=lambda i: (-(raw[i] - res[i]), i))
+    for i in order[:rem]:
+        res[i] += 1
+    return res
+
+
+def apportion_section_matrix(weights: Sequence[Sequence[float]], total_per_section: int):
+    """Row-wise largest remainder (P/qk_uncertainty_tangent_attention.py:1239-1264)."""
+    return [apportion(row, total_per_section) for row in weights]
+
+
+def budget_blocks(fraction: float, n_history_blocks: int) -> int:
+    """k = int(round(fraction * blocks)) (Python round-half-even),
+    as P/matrix_curvature_phase_frame_weave.py:5729."""
+    return int(round(fraction * n_history_blocks))
+
+
+# --------------------------------------------------------------------------
+# whole layer call
+
+def rcsa_layer(q, k, v, q_valid, k_valid, *, block_size: int, k_select, forced=None,
+               allowed=None, int8: bool = False, heads=None, qblocks=None):
+    """score -> select -> (quantise) -> sparse attention, all on the CPU.
+
+    Returns dict(score, indices, counts, out, lse[, q_i8, q_scale, k_i8, k_scale, kmean]).
+    """
+    qhat, _, _ = pool_blocks(q, q_valid, block_size)
+    khat, _, _ = pool_blocks(k, k_valid, block_size)
+    B, H = q.shape[:2]
+    score = block_scores(qhat, khat).reshape(B * H, qhat.shape[2], khat.shape[2])
+    idx, cnt = select_topk(score, k_select, forced=forced, allowed=allowed)
+    nq = qhat.shape[2]
+    idx4 = idx.reshape(B, H, nq, -1)
+    cnt3 = cnt.reshape(B, H, nq)
+    res = {"score": score, "indices": idx, "counts": cnt}
+    if int8:
+        q8, qs = quantize_query_blocks(q, q_valid, block_size)
+        km = key_mean(k, k_valid)
+        k8, ks = quantize_key_blocks(k, k_valid, block_size, km)
+        out, lse = sparse_attention_int8(q8, qs, k8, ks, v, idx4, cnt3, k_valid,
+                                         block_m=block_size, block_n=block_size,
+                                         heads=heads, qblocks=qblocks)
+        res.update(q_i8=q8, q_scale=qs, k_i8=k8, k_scale=ks, kmean=km)
+    else:
+        out, lse = sparse_attention(q, k, v, idx4, cnt3, k_valid, block_m=block_size,
+                                    block_n=block_size, heads=heads, qblocks=qblocks)
+    res.update(out=out, lse=lse)
+    return res
