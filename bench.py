@@ -1,0 +1,252 @@
+"""RCSA layer-call benchmark on one MI355X.
+
+Workload (the headline configuration): B=1, 24 heads x d128, 3520 query
+tokens (4 frames x 880), 35200 history tokens (40 frames) + the 3520-token
+current chunk as KV, 128-token blocks, 25% history budget (69 of 275 blocks)
+plus the always-kept current chunk, int8 Q/K (per-block symmetric scales, K
+mean-smoothed, 4 K channels x10 outliers), bf16 V, seeded synthetic data.
+
+A step is one layer call of the hot path: pooled Q (+ fused int8 Q
+quantiser), pooled K (+ smoothing statistics), block scores, top-k
+selection, int8 K quantiser, block-sparse attention.  Inputs are resident in
+HBM before the timed region.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+
+prints ONE JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
+BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_int8_dit_traffic.txt")
+
+
+def _events_time(fn, iters: int, warmup: int = 3) -> float:
+    """Average milliseconds of ``fn`` on the current stream (HIP events)."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(iters):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / iters
+
+
+def _read_traffic():
+    """HBM bytes per attention launch measured with rocprofv3 --pmc
+    (FETCH_SIZE + WRITE_SIZE, copy-kernel calibrated), if recorded."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(seed: int, heads: int) -> dict:
+    """The reference's PyTorch eager fp32 path (restated by the oracle) on the
+    host cores, on a bounded sample: ``heads`` of the 24 heads of the same
+    layer call; scaled to the full layer call."""
+    import torch
+    from cast_amd import workloads
+    from oracle import rcsa_oracle as orc
+    torch.set_num_threads(os.cpu_count() or 1)
+    w = workloads.matrix_dit(seed, int8=True)
+    q = w.q[:, :heads].float()
+    k = w.k[:, :heads].float()
+    v = w.v[:, :heads].float()
+
+    def run():
+        return orc.rcsa_layer(q, k, v, w.q_valid, w.k_valid, block_size=w.block_size,
+                              k_select=w.k_total, forced=w.forced)
+
+    run()  # warmup
+    times = []
+    res = None
+    for _ in range(3):
+        t0 = time.perf_counter()
+        res = run()
+        times.append(time.perf_counter() - t0)
+    sample_s = statistics.median(times)
+    full_s = sample_s * w.q.shape[1] / heads
+    ops = w.attention_ops(res["indices"].reshape(1, heads, w.n_qblocks, -1),
+                          res["counts"].reshape(1, heads, w.n_qblocks)) * w.q.shape[1] / heads
+    return {"value": ops / full_s / 1e12, "unit": "TOPS", "cores": torch.get_num_threads(),
+            "kind": "port", "ms_per_layer_call": full_s * 1e3,
+            "sample": f"{heads} of 24 heads of the same layer call (fp32 eager: pool, score, "
+                      f"top-k, masked softmax attention), median of 3 after 1 warmup, "
+                      f"scaled x{w.q.shape[1] / heads:g}"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-extras", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=8)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU (the RCSA path needs no collective; "
+              f"heads shard with no exchange); --gpus {args.gpus} is not supported",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from cast_amd import _lib, ops, workloads
+    from cast_amd.pipeline import rcsa_attention
+    _lib.load()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda:0")
+
+    w = workloads.matrix_dit(args.seed, int8=True).to(dev)
+    bs = w.block_size
+    max_k = w.k_total
+
+    def step():
+        return rcsa_attention(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=bs,
+                              k_select=w.k_total, forced=w.forced, int8=True, max_k=max_k)
+
+    for _ in range(args.warmup):
+        res = step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        res = step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ops_attn = w.attention_ops(res.indices, res.counts)
+    value = ops_attn / (ms_per_step * 1e-3) / 1e12
+
+    # ---- per-kernel timings with HIP events on the launch stream ----
+    iters = max(10, args.steps)
+    qhat, q8, qs = ops.pool_query(w.q, w.q_valid, bs, quantize=True)
+    khat, ksum, kmin, kmax = ops.pool_key(w.k, w.k_valid, bs, stats=True)
+    score = ops.block_scores(qhat, khat)
+    idx, cnt = ops.select_topk(score, w.k_total, forced=w.forced, max_k=max_k)
+    k8, ks, km = ops.quantize_key(w.k, w.k_valid, bs, ksum, kmin, kmax)
+    B, H, Lq, D = w.q.shape
+    idx4, cnt3 = idx.view(B, H, -1, max_k), cnt.view(B, H, -1)
+    out = torch.empty_like(w.q)
+    stage_ms = {
+        "pool_query_quant": _events_time(lambda: ops.pool_query(w.q, w.q_valid, bs, True), iters),
+        "pool_key_stats": _events_time(lambda: ops.pool_key(w.k, w.k_valid, bs, True), iters),
+        "block_scores": _events_time(lambda: ops.block_scores(qhat, khat), iters),
+        "select_topk": _events_time(lambda: ops.select_topk(score, w.k_total, forced=w.forced,
+                                                            max_k=max_k), iters),
+        "quantize_key": _events_time(lambda: ops.quantize_key(w.k, w.k_valid, bs, ksum, kmin,
+                                                              kmax), iters),
+        "sparse_attn_int8": _events_time(lambda: ops.sparse_attn_int8(
+            q8, qs, k8, ks, w.v, idx4, cnt3, w.k_valid, block_m=bs, block_n=bs, out=out), iters),
+    }
+    attn_ms = stage_ms["sparse_attn_int8"]
+    achieved = ops_attn / (attn_ms * 1e-3) / 1e12
+    qk_ops = pv_ops = ops_attn / 2
+    mixed_floor_ms = (qk_ops / (INT8_PEAK_TOPS * 1e12) + pv_ops / (BF16_PEAK_TFLOPS * 1e12)) * 1e3
+    el = w.q.element_size()
+    nbh = B * H
+    lk = w.k.shape[2]
+    hbm = {
+        "pool_query_quant": nbh * Lq * D * (el + 1),
+        "pool_key_stats": nbh * lk * D * el + 4 * nbh * w.n_kblocks * D * 4,
+        "quantize_key": nbh * lk * D * (el + 1) + 2 * nbh * w.n_kblocks * D * 4,
+    }
+    hbm_frac = {k_: {"GB/s": b / (stage_ms[k_] * 1e-3) / 1e9,
+                     "frac": b / (stage_ms[k_] * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                for k_, b in hbm.items()}
+
+    line = {
+        "metric": "block-sparse attn ms/layer-call + effective TOPS, int8-QK, 3.5k q x 35k KV",
+        "value": value,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": "rcsa_layer_call_int8qk_bf16pv", "batch": 1, "heads": H,
+                   "head_dim": D, "query_tokens": 3520, "history_tokens": 35200,
+                   "current_kv_tokens": 3520, "block_size": bs,
+                   "history_budget_blocks": w.k_hist, "history_blocks": w.n_hist_blocks,
+                   "blocks_per_row": w.k_total, "outlier_k_channels": 4},
+        "roofline": {"bound": "mfma", "achieved": achieved, "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": achieved / INT8_PEAK_TOPS,
+                     "traffic": _read_traffic(),
+                     "kernel": "sparse_attn_kernel<int8>", "ops_per_launch": ops_attn,
+                     "avg_launch_ms": attn_ms,
+                     "mixed_ceiling_frac": mixed_floor_ms / attn_ms},
+    }
+    extras = {"stage_ms": stage_ms, "hbm": hbm_frac, "ms_per_layer_call": ms_per_step}
+
+    if not args.no_extras:
+        # bf16-QK attention on the same shape (the drop-in kernel)
+        wb = workloads.matrix_dit(args.seed, int8=False).to(dev)
+        rb = rcsa_attention(wb.q, wb.k, wb.v, wb.q_valid, wb.k_valid, block_size=bs,
+                            k_select=wb.k_total, forced=wb.forced, int8=False, max_k=max_k)
+        outb = torch.empty_like(wb.q)
+        bf_ms = _events_time(lambda: ops.sparse_attn_bf16(
+            wb.q, wb.k, wb.v, rb.indices, rb.counts, wb.k_valid, block_m=bs, block_n=bs,
+            out=outb), iters)
+        bf_ops = wb.attention_ops(rb.indices, rb.counts)
+        extras["bf16_attn"] = {"ms": bf_ms, "TFLOP/s": bf_ops / bf_ms / 1e9,
+                               "frac_bf16_peak": bf_ops / bf_ms / 1e9 / BF16_PEAK_TFLOPS}
+        del wb, rb, outb
+        # per-denoising-step sweep: 30 layers, 1-4 anchor frames, 12.5-50% budget
+        plan = workloads.step_sweep_plan(args.seed)
+        layers = [workloads.step_layer_view(w, p) for p in plan]
+
+        def sweep():
+            r = []
+            for lw in layers:
+                r.append(rcsa_attention(lw.q, lw.k, lw.v, lw.q_valid, lw.k_valid,
+                                        block_size=bs, k_select=lw.k_total, forced=lw.forced,
+                                        int8=True, max_k=lw.k_total))
+            return r
+
+        sweep()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n_sweep = 3
+        for _ in range(n_sweep):
+            rs = sweep()
+        torch.cuda.synchronize()
+        step_ms = (time.perf_counter() - t0) * 1e3 / n_sweep
+        sweep_ops = sum(lw.attention_ops(r.indices, r.counts) for lw, r in zip(layers, rs))
+        extras["step_sweep_30_layers"] = {"ms_per_step": step_ms,
+                                          "effective_TOPS": sweep_ops / step_ms / 1e9}
+        del layers, rs
+
+    line["extras"] = extras
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(args.seed, args.cpu_heads)
+    print(json.dumps(line))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -182,26 +182,49 @@ score_kernel(const float* qhat, const float* khat, int64_t nq, int64_t nk,
 }
 
 // Per-head key mean over all valid tokens: kmean = sum_b ksum / n_valid_total.
+// One workgroup per head; the block loop is unrolled with independent
+// partial sums so that many loads are in flight (the pass is latency bound).
 template <int D>
 __global__ void __launch_bounds__(256)
 kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
              int64_t n_tokens, float* kmean) {
   constexpr int G = 256 / D;
+  constexpr int U = 8;
   __shared__ float part[G][D];
   __shared__ float s_red[4];
   const int64_t bh = blockIdx.x;
   const int t = threadIdx.x, c = t % D, g = t / D;
+  const float* src = ksum + bh * n_blocks * D + c;
+  float acc[U];
+#pragma unroll
+  for (int u = 0; u < U; ++u) acc[u] = 0.0f;
+  int64_t b = g;
+  for (; b + (U - 1) * G < n_blocks; b += U * G) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc[u] += src[(b + u * G) * D];
+  }
+  for (; b < n_blocks; b += G) acc[0] += src[b * D];
   float s = 0.0f;
-  for (int64_t b = g; b < n_blocks; b += G) s += ksum[(bh * n_blocks + b) * D + c];
+#pragma unroll
+  for (int u = 0; u < U; ++u) s += acc[u];
   part[g][c] = s;
   int cnt = 0;
-  for (int64_t i = t; i < n_tokens; i += 256) cnt += (valid == nullptr || valid[i] != 0);
+  if (valid == nullptr) {
+    cnt = t == 0 ? static_cast<int>(n_tokens) : 0;
+  } else {
+    int64_t i = t;
+    for (; i + 7 * 256 < n_tokens; i += 8 * 256) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) cnt += valid[i + u * 256] != 0;
+    }
+    for (; i < n_tokens; i += 256) cnt += valid[i] != 0;
+  }
   const float total = block_sum(static_cast<float>(cnt), s_red);
   if (t < D) {
-    float acc = 0.0f;
+    float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < G; ++i) acc += part[i][t];
-    kmean[bh * D + t] = acc / fmaxf(total, 1.0f);
+    for (int i = 0; i < G; ++i) sum += part[i][t];
+    kmean[bh * D + t] = sum / fmaxf(total, 1.0f);
   }
 }
 

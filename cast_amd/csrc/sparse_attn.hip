@@ -1,29 +1,44 @@
 // Block-sparse flash attention for gfx950 (MI355X).
 //
-// One workgroup = one (batch, head, query block) = BLOCK_M query rows, one
-// wavefront per 32 rows.  The workgroup streams only the key blocks named in
-// its block list: each selected K tile and V tile is staged in LDS once and
-// shared by all wavefronts.
+// Work decomposition: one workgroup = one (batch, head, query block) of
+// BLOCK_M rows; it streams only the key blocks named in its block list.
+// The workgroup has 2 * BLOCK_M / 32 wavefronts: row group rg (32 query
+// rows) x key half kh (BLOCK_N / 2 keys of every block).  The two key halves
+// keep independent online-softmax states that are merged once at the end, so
+// eight wavefronts share every staged tile (two per SIMD).
 //
-// Orientation: every wavefront computes S^T = K Q^T with 32x32 MFMAs, so a
-// lane owns ONE query row (column lane%32 of the MFMA output) and holds 16
-// of every 32 keys in registers.  Row max / row sum are then in-lane, plus a
-// single exchange with the partner lane (lane ^ 32).  The key rows fed to the
-// A operand are permuted (pi below) so that lane half h holds the 16
-// CONSECUTIVE keys 16h..16h+15 of each 32-key tile; P^T then feeds the B
-// operand of O^T = V^T P^T directly from registers, and the matching V^T
-// operand is one 16-byte LDS read.  V is transposed once while it is staged
-// into LDS.
+// Staging: each selected K tile (row-major, 16-byte chunks XOR-swizzled) and
+// V tile (row-major, swizzled) is copied global -> LDS with direct-to-LDS
+// loads (no VGPR round trip), double buffered: the copy of block i+1 is in
+// flight while block i is computed.
 //
-// QK^T runs on v_mfma_i32_32x32x32_i8 (int8 path) or
-// v_mfma_f32_32x32x16_bf16 (bf16 path); PV on v_mfma_f32_32x32x16_bf16.
-// Softmax is online, in fp32, in the exp2 domain (log2(e) folded into the
-// logit scale).
+// Orientation: a wavefront computes S^T = K Q^T with 32x32 MFMAs, so a lane
+// owns ONE query row (column lane%32 of the MFMA output).  The K rows fed to
+// the A operand are permuted (key_perm) so that lane half h holds the 16
+// consecutive keys 16h..16h+15 of each 32-key tile; P^T then feeds the B
+// operand of O^T = V^T P^T straight from registers.  The V^T operand comes
+// from the row-major V tile through ds_read_b64_tr_b16 (a 16-lane group
+// reading a 4x16 block receives its transpose).
+//
+// Arithmetic: QK^T on v_mfma_i32_32x32x32_i8 (int8) or
+// v_mfma_f32_32x32x16_bf16 (bf16); PV on v_mfma_f32_32x32x16_bf16.  In the
+// int8 path the i32 accumulator starts at the bit pattern of 1.5 * 2^23, so
+// the result read as fp32 is exactly 1.5 * 2^23 + x (|x| < 2^22): the
+// int->float conversion is free and folds into the exp2 argument's FMA.
+// Softmax is online, fp32, exp2 domain (log2(e) folded into the scale); the
+// running max is only moved when a row's max grows by more than 2^8
+// (rescaling O is skipped otherwise).  Row sums accumulate the bf16-rounded
+// probabilities with v_dot2_f32_bf16, so numerator and denominator use the
+// same P.
 #include <type_traits>
 
 #include "rcsa_common.h"
 
 namespace rcsa {
+
+typedef __bf16 v4bf __attribute__((ext_vector_type(4)));
+typedef __bf16 v2bf __attribute__((ext_vector_type(2)));
+#define RCSA_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
 
 struct AttnArgs {
   const void* q;
@@ -44,31 +59,55 @@ struct AttnArgs {
   int64_t H, q_len, k_len, n_qblocks, n_kblocks, max_k, n_work;
 };
 
-// Row permutation of the QK A operand (see header comment): MFMA row
-// m = 8a + 4h + b feeds key 16h + 4a + b.
+constexpr float kTau = 8.0f;               // lazy-rescale threshold, log2 units
+constexpr float kMagicF = 12582912.0f;     // 1.5 * 2^23
+constexpr int kMagicI = 0x4B400000;        // its fp32 bit pattern
+
+// MFMA row m = 8a + 4h + b of a 32-key tile reads key 16h + 4a + b.
 __device__ __forceinline__ int key_perm(int m) {
   return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
 }
-// 16-byte chunk swizzles that keep the LDS reads bank-conflict free.
+// 16-byte chunk swizzles (bank-conflict-free ds_read_b128 of permuted K rows,
+// balanced ds_read_b64_tr_b16 over 4-row groups of V).
 __device__ __forceinline__ int swz_k(int row) { return (row & 3) | ((row >> 2) & 4); }
-__device__ __forceinline__ int swz_v(int d) { return d + (d >> 3); }
+__device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
 
 template <bool INT8, int D, int BM, int BN>
-__global__ void __launch_bounds__(BM * 2)
-sparse_attn_kernel(AttnArgs a) {
-  constexpr int NT = BM * 2;                   // threads (BM/32 wavefronts)
-  constexpr int KB = INT8 ? 1 : 2;             // bytes per K element
-  constexpr int KROW = D * KB;                 // bytes per staged K row
-  constexpr int CPR_K = KROW / 16;             // 16-byte chunks per K row
-  constexpr int VROW = BN * 2;                 // bytes per staged V^T row
-  constexpr int CPR_V = BN / 8;
-  constexpr int QSTEPS = INT8 ? D / 32 : D / 16;
-  constexpr int NKT = BN / 32;                 // 32-key tiles per block
-  constexpr int NDT = D / 32;                  // 32-wide head_dim tiles
+struct AttnCfg {
+  static constexpr int NRG = BM / 32;            // row groups
+  static constexpr int NW = NRG * 2;             // wavefronts
+  static constexpr int NT = NW * 64;             // threads
+  static constexpr int KB = INT8 ? 1 : 2;        // bytes per K element
+  static constexpr int KROW = D * KB;            // bytes per staged K row
+  static constexpr int CPR_K = KROW / 16;
+  static constexpr int VROW = D * 2;             // bytes per staged V row
+  static constexpr int CPR_V = VROW / 16;
+  static constexpr int QSTEPS = INT8 ? D / 32 : D / 16;
+  static constexpr int HK = BN / 2;              // keys per wavefront per block
+  static constexpr int KT = HK / 32;             // 32-key tiles per wavefront
+  static constexpr int NDT = D / 32;             // 32-wide head_dim tiles
+  static constexpr int KBYTES = BN * KROW;
+  static constexpr int VBYTES = BN * VROW;
+  static constexpr int BUF = KBYTES + VBYTES;
+  static constexpr int UNITS = BUF / 1024;       // 1 KiB direct-load units
+  static constexpr int KUNITS = KBYTES / 1024;
+  static constexpr int UPW = (UNITS + NW - 1) / NW;
+  static constexpr int K_RPU = 1024 / KROW;      // rows per unit
+  static constexpr int V_RPU = 1024 / VROW;
+  static constexpr int MERGE_WAVE = NDT * 16 * 64 + 128;  // floats
+  static constexpr int MERGE = NRG * MERGE_WAVE * 4;     // bytes
+  static constexpr int SMEM = 2 * BUF > MERGE ? 2 * BUF : MERGE;
+  static_assert(KBYTES % 1024 == 0 && VBYTES % 1024 == 0, "tile is not whole 1 KiB units");
   static_assert(QSTEPS * 2 == CPR_K, "K chunk layout");
+};
 
-  __shared__ __attribute__((aligned(16))) char s_k[BN * KROW];
-  __shared__ __attribute__((aligned(16))) char s_v[D * VROW];
+template <bool INT8, int D, int BM, int BN>
+__global__ void __launch_bounds__(BM * 4)  // == AttnCfg::NT
+sparse_attn_kernel(AttnArgs a) {
+  using C = AttnCfg<INT8, D, BM, BN>;
+  typedef typename std::conditional<INT8, v4i, v8bf>::type OpT;
+  typedef typename std::conditional<INT8, v16i, v16f>::type AccT;
+  __shared__ __attribute__((aligned(1024))) char smem[C::SMEM];
 
   const int64_t work = xcd_remap(blockIdx.x, a.n_work);
   if (work < 0) return;
@@ -78,122 +117,137 @@ sparse_attn_kernel(AttnArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave, wave = tid / kWave;
+  const int rg = wave % C::NRG, kh = wave / C::NRG;
   const int hf = lane >> 5, lr = lane & 31;
-  const int64_t qrow = qb * BM + wave * 32 + lr;
+  const int64_t qrow = qb * BM + rg * 32 + lr;
   const bool qrow_ok = qrow < a.q_len;
 
-  // Q operand (B of S^T = K Q^T): lane holds 16 contiguous bytes per step,
-  // lane half hf covering the row's bytes [hf*KROW/2, (hf+1)*KROW/2).
-  typedef typename std::conditional<INT8, v4i, v8bf>::type OpT;
-  typedef typename std::conditional<INT8, v16i, v16f>::type AccT;
-  OpT q_op[QSTEPS];
+  // Q operand (B of S^T = K Q^T): lane half hf holds the row's bytes
+  // [hf*KROW/2, (hf+1)*KROW/2) as QSTEPS 16-byte steps.
+  OpT q_op[C::QSTEPS];
   {
     const char* qp = static_cast<const char*>(a.q) +
-                     (b * a.sqz + h * a.sqh + qrow * a.sqm) * KB;
+                     (b * a.sqz + h * a.sqh + qrow * a.sqm) * C::KB;
 #pragma unroll
-    for (int st = 0; st < QSTEPS; ++st) {
+    for (int st = 0; st < C::QSTEPS; ++st) {
       v4i raw = {0, 0, 0, 0};
-      if (qrow_ok) raw = *reinterpret_cast<const v4i*>(qp + (hf * QSTEPS + st) * 16);
+      if (qrow_ok) raw = *reinterpret_cast<const v4i*>(qp + (hf * C::QSTEPS + st) * 16);
       q_op[st] = __builtin_bit_cast(OpT, raw);
     }
   }
   const float qs = INT8 ? a.q_scale[bh * a.q_scale_stride + qb] : 1.0f;
 
-  v16f o_acc[NDT];
+  v16f o_acc[C::NDT];
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
+  for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o_acc[dt][r] = 0.0f;
-  float m_run = -INFINITY;  // running max, log2 domain
-  float l_run = 0.0f;       // partial row sum over this lane's keys
+  float m_run = -INFINITY;  // running max (log2 domain), shared by both lane halves
+  float l_run = 0.0f;       // this lane's partial row sum
 
   int64_t cnt = a.lens[b * a.slz + h * a.slh + qb * a.slm];
   cnt = cnt < 0 ? 0 : (cnt > a.max_k ? a.max_k : cnt);
   const int32_t* list = a.idx + b * a.sbz + h * a.sbh + qb * a.sbm;
+  const char* kbase = static_cast<const char*>(a.k) + (b * a.skz + h * a.skh) * C::KB;
+  const char* vbase = reinterpret_cast<const char*>(a.v + b * a.svz + h * a.svh);
+  const int64_t klast = a.k_len - 1;
+  const int64_t krow_bytes = a.skn * C::KB, vrow_bytes = a.svn * 2;
 
-  const char* kbase = static_cast<const char*>(a.k) + (b * a.skz + h * a.skh) * KB;
-  const u16* vbase = a.v + b * a.svz + h * a.svh;
+  // Direct-to-LDS staging geometry.  Unit u (1 KiB) of a buffer holds K rows
+  // (u < KUNITS) or V rows; lane l lands at byte l*16 of its unit, so it
+  // loads the swizzled global chunk that belongs there.  Per unit: the tile
+  // row this lane copies and that row's in-row byte offset (32-bit: the host
+  // bounds one head's K/V below 2 GiB).
+  int st_row[C::UPW];
+  int st_col[C::UPW];
+#pragma unroll
+  for (int i = 0; i < C::UPW; ++i) {
+    const int u = wave * C::UPW + i;
+    if (u < C::KUNITS) {
+      st_row[i] = u * C::K_RPU + lane / C::CPR_K;
+      st_col[i] = ((lane % C::CPR_K) ^ (swz_k(st_row[i]) & (C::CPR_K - 1))) * 16;
+    } else {
+      st_row[i] = (u - C::KUNITS) * C::V_RPU + lane / C::CPR_V;
+      st_col[i] = ((lane % C::CPR_V) ^ (swz_v(st_row[i]) & (C::CPR_V - 1))) * 16;
+    }
+  }
+  // Rows past k_len re-read the last row (those keys are masked).
+  auto stage = [&](int64_t n, int buf) {
+    const int64_t key0 = n * BN;
+    const bool tail = key0 + BN > a.k_len;
+    char* dst = smem + buf * C::BUF;
+#pragma unroll
+    for (int i = 0; i < C::UPW; ++i) {
+      const int u = wave * C::UPW + i;
+      if (u < C::UNITS) {
+        int64_t key = key0 + st_row[i];
+        if (tail) key = min(key, klast);
+        const char* src = u < C::KUNITS
+            ? kbase + static_cast<uint32_t>(key * krow_bytes + st_col[i])
+            : vbase + static_cast<uint32_t>(key * vrow_bytes + st_col[i]);
+        __builtin_amdgcn_global_load_lds(src, RCSA_LDS(void, dst + u * 1024), 16, 0, 0);
+      }
+    }
+  };
+  auto block_of = [&](int64_t it) -> int64_t {
+    const int64_t n = list[it];
+    return (n >= 0 && n < a.n_kblocks) ? n : 0;
+  };
+
+  // Lane-dependent LDS read offsets.  The swizzles only involve lane bits,
+  // so tile/step offsets (32t, 8u, 4q rows) become instruction immediates.
+  int k_off[C::QSTEPS];
+  {
+    const int row = key_perm(lr);  // + kh*HK + 32t: multiples of 32
+    const int sw = swz_k(row) & (C::CPR_K - 1);
+#pragma unroll
+    for (int st = 0; st < C::QSTEPS; ++st)
+      k_off[st] = (kh * C::HK + row) * C::KROW + (((hf * C::QSTEPS + st) ^ sw) * 16);
+  }
+  int v_off[C::NDT];
+  {
+    const int grp = lane >> 4, gi = lane & 15;
+    const int row = 16 * (grp >> 1) + (gi >> 2);  // + kh*HK + 32t + 8u + 4q: multiples of 4
+    const int sw = swz_v(row) & (C::CPR_V - 1);
+#pragma unroll
+    for (int dt = 0; dt < C::NDT; ++dt) {
+      const int d = 32 * dt + 16 * (grp & 1) + 4 * (gi & 3);
+      v_off[dt] = C::KBYTES + (kh * C::HK + row) * C::VROW + (((d >> 3) ^ sw) * 16) + (d & 7) * 2;
+    }
+  }
+
+  if (cnt > 0) stage(block_of(0), 0);
 
   for (int64_t it = 0; it < cnt; ++it) {
-    const int64_t n = list[it];
-    if (n < 0 || n >= a.n_kblocks) continue;  // uniform across the workgroup
-    const int64_t key0 = n * BN;
+    const int64_t n_raw = list[it];
+    const bool blk_ok = n_raw >= 0 && n_raw < a.n_kblocks;
+    const int64_t n = blk_ok ? n_raw : 0;
+    const int buf = static_cast<int>(it & 1);
+    __syncthreads();  // block `it` is in LDS; everyone is done with the other buffer
+    if (it + 1 < cnt) stage(block_of(it + 1), buf ^ 1);
 
-    __syncthreads();  // previous tile fully consumed
-    // ---- stage K (row-major, chunk-swizzled) ----
-#pragma unroll
-    for (int pass = 0; pass < (BN * CPR_K + NT - 1) / NT; ++pass) {
-      const int e = tid + pass * NT;
-      if (e >= BN * CPR_K) break;
-      const int row = e / CPR_K, c = e % CPR_K;
-      v4i val = {0, 0, 0, 0};
-      if (key0 + row < a.k_len)
-        val = *reinterpret_cast<const v4i*>(kbase + (key0 + row) * a.skn * KB + c * 16);
-      *reinterpret_cast<v4i*>(s_k + row * KROW + ((c ^ (swz_k(row) & (CPR_K - 1))) * 16)) = val;
-    }
-    // ---- stage V transposed: s_v[d][key] ----
-#pragma unroll
-    for (int pass = 0; pass < ((BN / 4) * (D / 8) + NT - 1) / NT; ++pass) {
-      const int e = tid + pass * NT;
-      if (e >= (BN / 4) * (D / 8)) break;
-      const int dc = e % (D / 8), kg = e / (D / 8);
-      uint4 r4[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int64_t key = key0 + 4 * kg + i;
-        r4[i] = key < a.k_len
-                    ? *reinterpret_cast<const uint4*>(vbase + key * a.svn + dc * 8)
-                    : make_uint4(0, 0, 0, 0);
-      }
-#pragma unroll
-      for (int dp = 0; dp < 8; ++dp) {
-        uint32_t x[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t w = (dp >> 1) == 0 ? r4[i].x : (dp >> 1) == 1 ? r4[i].y
-                           : (dp >> 1) == 2 ? r4[i].z : r4[i].w;
-          x[i] = w;
-        }
-        uint32_t lo, hi;
-        if (dp & 1) {
-          lo = (x[0] >> 16) | (x[1] & 0xffff0000u);
-          hi = (x[2] >> 16) | (x[3] & 0xffff0000u);
-        } else {
-          lo = (x[0] & 0xffffu) | (x[1] << 16);
-          hi = (x[2] & 0xffffu) | (x[3] << 16);
-        }
-        const int d = dc * 8 + dp;
-        const int chunk = (kg >> 1) ^ (swz_v(d) & (CPR_V - 1));
-        *reinterpret_cast<uint2*>(s_v + d * VROW + chunk * 16 + (kg & 1) * 8) =
-            make_uint2(lo, hi);
-      }
-    }
-    // ---- key validity of this block (uniform bitmasks) ----
-    uint64_t vmask[(BN + 63) / 64];
-    bool all_valid = true;
-#pragma unroll
-    for (int w = 0; w < (BN + 63) / 64; ++w) {
-      const int64_t key = key0 + w * 64 + lane;
-      const bool ok = (w * 64 + lane < BN) && key < a.k_len &&
-                      (a.kvalid == nullptr || a.kvalid[key] != 0);
-      vmask[w] = __ballot(ok);
-      const uint64_t full = (BN - w * 64 >= 64) ? ~0ull : ((1ull << (BN - w * 64)) - 1ull);
-      all_valid = all_valid && (vmask[w] == full);
-    }
-    __syncthreads();
+    const char* tile = smem + buf * C::BUF;
+    const int64_t key0 = n * BN + kh * C::HK;
+
+    // validity of this wavefront's HK keys as a uniform bitmask
+    const int64_t mykey = key0 + lane;
+    const bool kok = blk_ok && lane < C::HK && mykey < a.k_len &&
+                     (a.kvalid == nullptr || a.kvalid[mykey] != 0);
+    const uint64_t vmask = __ballot(kok);
+    const bool all_valid = vmask == (C::HK == 64 ? ~0ull : ((1ull << C::HK) - 1ull));
 
     // ---- S^T = K Q^T ----
-    AccT s_acc[NKT];
+    AccT s_acc[C::KT];
 #pragma unroll
-    for (int t = 0; t < NKT; ++t) {
+    for (int t = 0; t < C::KT; ++t) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s_acc[t][r] = 0;
-      const int row = 32 * t + key_perm(lr);
-      const char* rp = s_k + row * KROW;
-      const int sw = swz_k(row) & (CPR_K - 1);
+      for (int r = 0; r < 16; ++r) {
+        if constexpr (INT8) s_acc[t][r] = kMagicI;
+        else s_acc[t][r] = 0.0f;
+      }
 #pragma unroll
-      for (int st = 0; st < QSTEPS; ++st) {
-        const v4i raw = *reinterpret_cast<const v4i*>(rp + (((hf * QSTEPS + st) ^ sw) * 16));
+      for (int st = 0; st < C::QSTEPS; ++st) {
+        const v4i raw = *reinterpret_cast<const v4i*>(tile + k_off[st] + 32 * t * C::KROW);
         if constexpr (INT8) {
           s_acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(raw, q_op[st], s_acc[t], 0, 0, 0);
         } else {
@@ -203,101 +257,127 @@ sparse_attn_kernel(AttnArgs a) {
       }
     }
 
-    // ---- online softmax (lane half hf, register r <-> key 32t + 16hf + r) ----
-    const float c = INT8 ? a.scale_log2 * qs * a.k_scale[bh * a.k_scale_stride + n]
-                         : a.scale_log2;
-    float p[NKT][16];
-    float mx = -INFINITY;
-    if (all_valid) {
-      if constexpr (INT8) {
-        int mi = INT32_MIN;
+    // ---- online softmax: lane half hf, register r <-> key 32t + 16hf + r ----
+    // raw value: int8 -> 1.5*2^23 + x read as fp32; bf16 -> the fp32 logit.
+    // A masked key's raw value becomes -inf, so max and exp2 need no mask.
+    float rv[C::KT][16];
 #pragma unroll
-        for (int t = 0; t < NKT; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mi = max(mi, s_acc[t][r]);
-        mx = static_cast<float>(mi) * c;
-      } else {
-#pragma unroll
-        for (int t = 0; t < NKT; ++t)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s_acc[t][r]);
-        mx *= c;
-      }
-    } else {
-#pragma unroll
-      for (int t = 0; t < NKT; ++t)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 32 * t + 16 * hf + r;
-          const bool ok = (vmask[kk >> 6] >> (kk & 63)) & 1ull;
-          const float x = static_cast<float>(s_acc[t][r]) * c;
-          mx = ok ? fmaxf(mx, x) : mx;
-        }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
-    // A row with nothing admissible so far keeps m = -inf, alpha = 1 and
-    // p = 0 (masked lanes are zeroed below); no divergent branch around MFMA.
-    const float m_new = fmaxf(m_run, mx);
-    const bool live = m_new != -INFINITY;
-    const float alpha = live ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
-    const float m_sub = live ? m_new : 0.0f;
-    m_run = m_new;
-    float lsum = 0.0f;
-#pragma unroll
-    for (int t = 0; t < NKT; ++t)
+    for (int t = 0; t < C::KT; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float e = __builtin_amdgcn_exp2f(static_cast<float>(s_acc[t][r]) * c - m_sub);
-        if (!all_valid) {
-          const int kk = 32 * t + 16 * hf + r;
-          e = ((vmask[kk >> 6] >> (kk & 63)) & 1ull) ? e : 0.0f;
-        }
-        p[t][r] = e;
-        lsum += e;
+        if constexpr (INT8) rv[t][r] = __int_as_float(s_acc[t][r]);
+        else rv[t][r] = s_acc[t][r];
       }
-    l_run = l_run * alpha + lsum;
+    if (!all_valid) {
+      // this lane's 16 keys of each tile as one 32-bit word
+      uint32_t bits = 0;
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+      for (int t = 0; t < C::KT; ++t)
+        bits |= static_cast<uint32_t>((vmask >> (32 * t + 16 * hf)) & 0xffffull) << (16 * t);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
+      for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          rv[t][r] = ((bits >> (16 * t + r)) & 1u) ? rv[t][r] : -INFINITY;
+    }
+    float rmax = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, rv[t][r]);
+    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, kWave));
+    const float c = INT8 ? a.scale_log2 * qs * a.k_scale[bh * a.k_scale_stride + n]
+                         : a.scale_log2;
+    const float m_blk = (rmax == -INFINITY) ? -INFINITY
+                        : (INT8 ? (rmax - kMagicF) * c : rmax * c);
+    if (__ballot(m_blk > m_run + kTau) != 0) {  // wavefront-uniform
+      const float m_new = fmaxf(m_run, m_blk);
+      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
+      m_run = m_new;
+    }
+    const float bias = -(INT8 ? c * kMagicF : 0.0f) - (m_run == -INFINITY ? 0.0f : m_run);
 
-    // ---- O^T += V^T P^T ----
+    v8bf p_op[C::KT][2];
 #pragma unroll
-    for (int t = 0; t < NKT; ++t) {
+    for (int t = 0; t < C::KT; ++t)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        v8bf p_op;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) p_op[j] = static_cast<__bf16>(p[t][8 * u + j]);
-        const int chunk = 4 * t + 2 * hf + u;
+        for (int j = 0; j < 8; ++j) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + j], c, bias));
+          p_op[t][u][j] = static_cast<__bf16>(e);
+        }
 #pragma unroll
-        for (int dt = 0; dt < NDT; ++dt) {
-          const int d = 32 * dt + lr;
-          const v8bf v_op = *reinterpret_cast<const v8bf*>(
-              s_v + d * VROW + ((chunk ^ (swz_v(d) & (CPR_V - 1))) * 16));
-          o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_op, p_op, o_acc[dt], 0, 0, 0);
+        for (int j = 0; j < 4; ++j) {
+          const v2bf pair = {p_op[t][u][2 * j], p_op[t][u][2 * j + 1]};
+          const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
+          l_run = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_run, false);
         }
       }
-    }
+
+    // ---- O^T += V^T P^T, V^T operand by transposing LDS reads ----
+#pragma unroll
+    for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt) {
+          const char* p0 = tile + v_off[dt] + (32 * t + 8 * u) * C::VROW;
+          const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0));
+          const v4bf hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+              RCSA_LDS(v4bf, p0 + 4 * C::VROW));
+          const v8bf v_op = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+          o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_op, p_op[t][u], o_acc[dt],
+                                                             0, 0, 0);
+        }
   }
 
-  // ---- epilogue: normalise, write O (bf16) and the log-sum-exp ----
+  // ---- merge the two key halves, normalise, write O (bf16) and the LSE ----
   const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (qrow_ok) {
-    u16* op = a.out + b * a.soz + h * a.soh + qrow * a.som;
+  __syncthreads();  // main loop done everywhere: LDS is free for the merge
+  float* mbuf = reinterpret_cast<float*>(smem) + rg * C::MERGE_WAVE;
+  if (kh == 1) {
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
+    for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d0 = 32 * dt + 8 * g + 4 * hf;
-        const uint32_t lo = pack_bf16x2(o_acc[dt][4 * g] * inv, o_acc[dt][4 * g + 1] * inv);
-        const uint32_t hi = pack_bf16x2(o_acc[dt][4 * g + 2] * inv, o_acc[dt][4 * g + 3] * inv);
-        *reinterpret_cast<uint2*>(op + d0) = make_uint2(lo, hi);
-      }
-    if (a.lse && hf == 0) {
-      a.lse[(b * a.H + h) * a.q_len + qrow] =
-          l_tot > 0.0f ? (m_run + __log2f(l_tot)) * 0.69314718055994531f : -INFINITY;
+      for (int r = 0; r < 16; ++r) mbuf[(dt * 16 + r) * 64 + lane] = o_acc[dt][r];
+    mbuf[C::NDT * 16 * 64 + lane] = m_run;
+    mbuf[C::NDT * 16 * 64 + 64 + lane] = l_tot;
+  }
+  __syncthreads();
+  if (kh == 0) {
+    const float m_b = mbuf[C::NDT * 16 * 64 + lane];
+    const float l_b = mbuf[C::NDT * 16 * 64 + 64 + lane];
+    const float m = fmaxf(m_run, m_b);
+    const float wa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+    const float wb = m_b == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_b - m);
+    const float l = l_tot * wa + l_b * wb;
+    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+    const float fa = wa * inv, fb = wb * inv;
+    if (qrow_ok) {
+      u16* op = a.out + b * a.soz + h * a.soh + qrow * a.som;
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          float o4[4];
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * g + j;
+            o4[j] = o_acc[dt][r] * fa + mbuf[(dt * 16 + r) * 64 + lane] * fb;
+          }
+          const int d0 = 32 * dt + 8 * g + 4 * hf;
+          *reinterpret_cast<uint2*>(op + d0) =
+              make_uint2(pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3]));
+        }
+      if (a.lse && hf == 0)
+        a.lse[(b * a.H + h) * a.q_len + qrow] =
+            l > 0.0f ? (m + __log2f(l)) * 0.69314718055994531f : -INFINITY;
     }
   }
 }
@@ -305,10 +385,11 @@ sparse_attn_kernel(AttnArgs a) {
 template <bool INT8>
 static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(xcd_grid(a.n_work)));
-#define RCSA_ATTN(D_, BM_, BN_)                                            \
-  if (D == D_ && BM == BM_ && BN == BN_) {                                 \
-    sparse_attn_kernel<INT8, D_, BM_, BN_><<<grid, dim3(BM_ * 2), 0, s>>>(a); \
-    return launch_status();                                                \
+#define RCSA_ATTN(D_, BM_, BN_)                                                   \
+  if (D == D_ && BM == BM_ && BN == BN_) {                                        \
+    sparse_attn_kernel<INT8, D_, BM_, BN_>                                        \
+        <<<grid, dim3(AttnCfg<INT8, D_, BM_, BN_>::NT), 0, s>>>(a);               \
+    return launch_status();                                                       \
   }
   RCSA_ATTN(128, 128, 128)
   RCSA_ATTN(128, 128, 64)
@@ -334,12 +415,13 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   if (B <= 0 || H <= 0 || Q_LEN <= 0 || K_LEN <= 0 || max_k < 0) return RCSA_ERR_SHAPE;
   if (!(D == 64 || D == 128) || !(BM == 64 || BM == 128) || !(BN == 64 || BN == 128))
     return RCSA_ERR_SHAPE;
+  if (!(sm_scale > 0.0f) || !(sm_scale < INFINITY)) return RCSA_ERR_SHAPE;
   // 16-byte aligned rows: bf16 strides multiple of 8, int8 multiple of 16
   if (sqm % kvec || sqh % kvec || sqz % kvec) return RCSA_ERR_STRIDE;
   if (skn % kvec || skh % kvec || skz % kvec) return RCSA_ERR_STRIDE;
   if (svn % 8 || svh % 8 || svz % 8) return RCSA_ERR_STRIDE;
   if (som % 4 || soh % 4 || soz % 4) return RCSA_ERR_STRIDE;
-  if (!aligned16(Out) && (reinterpret_cast<uintptr_t>(Out) & 7u)) return RCSA_ERR_ALIGN;
+  if (reinterpret_cast<uintptr_t>(Out) & 7u) return RCSA_ERR_ALIGN;
   a.kvalid = K_valid;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.lse = M;

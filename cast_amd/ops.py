@@ -42,15 +42,23 @@ def _require_cuda(fn: str, *tensors: Optional[torch.Tensor]) -> None:
             raise RuntimeError(f"{fn}: tensors must live on a HIP device, got {t.device}")
 
 
+def _bytes_mask(m: torch.Tensor, device) -> torch.Tensor:
+    """A one-byte-per-entry mask on ``device``: bool (stored as 0/1 bytes) and
+    uint8 pass through without a conversion kernel."""
+    if m.dtype not in (torch.bool, torch.uint8):
+        m = m != 0
+    if m.device != device:
+        m = m.to(device)
+    return m.contiguous()
+
+
 def _valid_u8(valid: Optional[torch.Tensor], n: int, device, fn: str) -> Optional[torch.Tensor]:
     if valid is None:
         return None
     v = valid.reshape(-1)
     if v.numel() != n:
         raise ValueError(f"{fn}: valid mask has {v.numel()} entries, expected {n}")
-    if v.dtype != torch.uint8:
-        v = v.to(torch.uint8)
-    return v.to(device).contiguous()
+    return _bytes_mask(v, device)
 
 
 def _bhld(x: torch.Tensor, block_size: int, fn: str) -> tuple[int, int, int, int, int]:
@@ -133,7 +141,7 @@ def _mask_u8(mask: Optional[torch.Tensor], nbh: int, nq: int, nk: int, device, f
     """Return (uint8 mask, head stride) for a [NQ, NK] or [NBH, NQ, NK] mask."""
     if mask is None:
         return None, 0
-    m = mask.to(device=device, dtype=torch.uint8)
+    m = _bytes_mask(mask, device)
     if m.shape == (nq, nk):
         return m.contiguous(), 0
     if m.shape == (nbh, nq, nk):

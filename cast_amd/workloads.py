@@ -62,12 +62,12 @@ class Workload:
     def attention_ops(self, indices: torch.Tensor, counts: torch.Tensor) -> float:
         """Algorithmic ops of the sparse attention: sum over heads and valid
         query rows of 2*D*(valid selected keys), once for QK^T and once for PV."""
-        B, H, _, D = self.q.shape
+        D = self.q.shape[3]
         bs = self.block_size
         kv_blocks = self.k_valid.reshape(-1, bs).sum(-1).to(torch.float64).cpu()
         q_rows = self.q_valid.reshape(-1, bs).sum(-1).to(torch.float64).cpu()
-        idx = indices.reshape(B * H, self.n_qblocks, -1).cpu().long()
-        cnt = counts.reshape(B * H, self.n_qblocks).cpu().long()
+        idx = indices.reshape(-1, self.n_qblocks, indices.shape[-1]).cpu().long()
+        cnt = counts.reshape(-1, self.n_qblocks).cpu().long()
         slot = torch.arange(idx.shape[-1])[None, None, :] < cnt[..., None]
         keys = torch.where(slot, kv_blocks[idx.clamp_min(0)], torch.zeros(()))
         keys_per_row = keys.sum(-1)                     # [BH, NQB]
@@ -257,6 +257,41 @@ def step_sweep_plan(seed: int = 0, layers: int = 30) -> list[dict]:
     fracs = torch.tensor([0.125, 0.25, 0.5])[torch.randint(0, 3, (layers,), generator=g)]
     return [{"layer": i, "query_frames": int(frames[i]), "fraction": float(fracs[i])}
             for i in range(layers)]
+
+
+def step_layer_view(base: Workload, plan: dict) -> Workload:
+    """Derive one sweep layer from a 4-frame DiT workload without regenerating:
+    queries = the first ``query_frames`` frames, current KV = the same frames,
+    history unchanged, budget = round(fraction * history blocks).  Works on
+    whatever device ``base`` lives on."""
+    bs = base.block_size
+    nf = int(plan["query_frames"])
+    lq = nf * FRAME_TOKENS
+    nqb = -(-lq // bs)
+    nhb = base.n_hist_blocks
+    lh = nhb * bs
+    dev = base.q.device
+    q = base.q[:, :, : nqb * bs].clone()
+    q[:, :, lq:] = 0
+    cur = base.k.shape[2] - lh
+    take = min(nqb * bs, cur)
+    k = torch.zeros(*base.k.shape[:2], lh + nqb * bs, base.k.shape[3], dtype=base.k.dtype,
+                    device=dev)
+    v = torch.zeros_like(k)
+    k[:, :, : lh + take] = base.k[:, :, : lh + take]
+    v[:, :, : lh + take] = base.v[:, :, : lh + take]
+    k[:, :, lh + lq:] = 0
+    v[:, :, lh + lq:] = 0
+    q_valid = torch.zeros(nqb * bs, dtype=torch.bool, device=dev)
+    q_valid[:lq] = True
+    k_valid = torch.zeros(lh + nqb * bs, dtype=torch.bool, device=dev)
+    k_valid[: lh] = base.k_valid[: lh]
+    k_valid[lh: lh + lq] = True
+    forced = torch.zeros(nqb, nhb + nqb, dtype=torch.bool, device=dev)
+    forced[:, nhb:] = True
+    return Workload(f"step_layer{plan['layer']}_f{nf}_b{plan['fraction']}", q, k, v, q_valid,
+                    k_valid, bs, nhb, budget_blocks(plan["fraction"], nhb), forced, True,
+                    dict(plan))
 
 
 def step_layer(plan: dict, seed: int = 0, *, heads: int = 24, head_dim: int = 128,
