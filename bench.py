@@ -107,6 +107,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=8)
+    ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy"], default=None,
+                    help="profiling mode: run only this kernel (--steps launches after "
+                         "--warmup) plus nothing else, and print its average time")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (the RCSA path needs no collective; "
@@ -120,9 +123,36 @@ def main() -> int:
     _lib.load()  # fail loudly if the HIP library is missing
     dev = torch.device("cuda:0")
 
-    w = workloads.matrix_dit(args.seed, int8=True).to(dev)
+    if args.only == "copy":
+        # calibration for HBM byte counters: a plain 1 GiB device copy
+        src = torch.empty(1 << 28, device=dev, dtype=torch.float32).fill_(1.0)
+        dst = torch.empty_like(src)
+        ms = _events_time(lambda: dst.copy_(src), args.steps, args.warmup)
+        print(json.dumps({"only": "copy", "bytes_read": src.numel() * 4,
+                          "bytes_written": dst.numel() * 4, "avg_ms": ms}))
+        return 0
+
+    w = workloads.matrix_dit(args.seed, int8=args.only != "attn_bf16").to(dev)
     bs = w.block_size
     max_k = w.k_total
+
+    if args.only is not None:
+        r = rcsa_attention(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=bs,
+                           k_select=w.k_total, forced=w.forced, int8=w.int8, max_k=max_k)
+        out = torch.empty_like(w.q)
+        if w.int8:
+            fn = lambda: ops.sparse_attn_int8(r.q_i8, r.q_scale, r.k_i8, r.k_scale, w.v,  # noqa
+                                              r.indices, r.counts, w.k_valid, block_m=bs,
+                                              block_n=bs, out=out)
+        else:
+            fn = lambda: ops.sparse_attn_bf16(w.q, w.k, w.v, r.indices, r.counts,  # noqa
+                                              w.k_valid, block_m=bs, block_n=bs, out=out)
+        torch.cuda.synchronize()
+        ms = _events_time(fn, args.steps, args.warmup)
+        ops_attn = w.attention_ops(r.indices, r.counts)
+        print(json.dumps({"only": args.only, "avg_ms": ms, "ops": ops_attn,
+                          "TOPS": ops_attn / ms / 1e9}))
+        return 0
 
     def step():
         return rcsa_attention(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=bs,

@@ -43,16 +43,54 @@ COMMON_FLAGS = [
 
 
 def _compile(src: Path, obj: Path) -> None:
-    cmd = [hipcc(), *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *COMMON_FLAGS, "-Rpass-analysis=kernel-resource-usage",
+           "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
-    err = "\n".join(
-        line for line in res.stderr.splitlines()
-        if "packed-fp32-ops" not in line  # host pass does not know the feature
-    )
+    lines = [line for line in res.stderr.splitlines()
+             if "packed-fp32-ops" not in line]  # host pass does not know the feature
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {src.name}:\n{err}")
-    if err.strip():
-        print(err, file=sys.stderr)
+        raise RuntimeError(f"hipcc failed for {src.name}:\n" + "\n".join(lines))
+    _check_resources(src, lines)
+    other = [line for line in lines if "remark:" not in line and line.strip()
+             and not line.lstrip().startswith(("|", "^")) and not line[:1].isdigit()]
+    if other:
+        print("\n".join(other), file=sys.stderr)
+    _check_stubs(obj)
+
+
+def _check_resources(src: Path, lines: list[str]) -> None:
+    """Fail if a kernel spills or uses scratch memory: the hot kernels are
+    written to live in registers and LDS, and a silent fall-back to scratch
+    (e.g. an un-inlined lambda) costs an order of magnitude."""
+    kernel = None
+    bad = []
+    for line in lines:
+        if "Function Name:" in line:
+            kernel = line.split("Function Name:")[1].split()[0]
+        elif "ScratchSize [bytes/lane]:" in line or "VGPRs Spill:" in line:
+            val = int(line.split(":")[-1].split()[0])
+            if val:
+                bad.append(f"{kernel}: {line.split('remark:')[1].split('[')[0].strip()}")
+    if bad:
+        raise RuntimeError(f"{src.name}: kernels spill or use scratch:\n  " + "\n  ".join(bad))
+
+
+def _check_stubs(obj: Path) -> None:
+    """Fail if the host pass left a kernel launch stub undefined.
+
+    hipcc can drop a template kernel's host stub without any diagnostic
+    (the library then links but fails to load with an undefined
+    ``__device_stub__`` symbol); catch that at build time.
+    """
+    nm = shutil.which("nm")
+    if nm is None:
+        return
+    res = subprocess.run([nm, str(obj)], capture_output=True, text=True)
+    missing = [line.split()[-1] for line in res.stdout.splitlines()
+               if " U " in line and "__device_stub__" in line]
+    if missing:
+        raise RuntimeError(f"{obj.name}: host pass left kernel stubs undefined: "
+                           f"{missing[:4]}{' ...' if len(missing) > 4 else ''}")
 
 
 def build(verbose: bool = True) -> Path:

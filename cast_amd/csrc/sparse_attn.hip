@@ -72,10 +72,49 @@ __device__ __forceinline__ int key_perm(int m) {
 __device__ __forceinline__ int swz_k(int row) { return (row & 3) | ((row >> 2) & 4); }
 __device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
 
-template <bool INT8, int D, int BM, int BN>
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding:
+// vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at [15:14]).
+constexpr int vmcnt_imm(int n) {
+  return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 0x3) << 14);
+}
+
+// Load through the constant address space: read-only inputs (block lists,
+// scales) then go through the scalar unit (lgkmcnt) instead of a vector load
+// whose vmcnt wait would also drain the direct-to-LDS copies in flight.
+template <typename T>
+__device__ __forceinline__ T ld_const(const T* p) {
+  return *(const __attribute__((address_space(4))) T*)(p);
+}
+
+// Wait until at most N vector-memory operations of this wavefront are
+// outstanding, then barrier the workgroup.  Unlike __syncthreads(), whose
+// workgroup fences drain every outstanding direct-to-LDS copy, this keeps the
+// younger ring stages in flight.  The memory clobber keeps the compiler from
+// moving LDS accesses across it.
+template <int N>
+__device__ __forceinline__ void wait_vm_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+// v[lane] + v[lane ^ 32] through v_permlane32_swap.
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                   false, false);
+  return __uint_as_float(sw[0]) + __uint_as_float(sw[1]);
+}
+
+// max(v[lane], v[lane ^ 32]) through v_permlane32_swap (no LDS round trip).
+__device__ __forceinline__ float pair_max(float v) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                   false, false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
+template <bool INT8, int D, int BM, int BN, int STAGES>
 struct AttnCfg {
   static constexpr int NRG = BM / 32;            // row groups
-  static constexpr int NW = NRG * 2;             // wavefronts
+  static constexpr int NW = NRG * 2;             // wavefronts: row group x key half
   static constexpr int NT = NW * 64;             // threads
   static constexpr int KB = INT8 ? 1 : 2;        // bytes per K element
   static constexpr int KROW = D * KB;            // bytes per staged K row
@@ -88,26 +127,36 @@ struct AttnCfg {
   static constexpr int NDT = D / 32;             // 32-wide head_dim tiles
   static constexpr int KBYTES = BN * KROW;
   static constexpr int VBYTES = BN * VROW;
-  static constexpr int BUF = KBYTES + VBYTES;
-  static constexpr int UNITS = BUF / 1024;       // 1 KiB direct-load units
-  static constexpr int KUNITS = KBYTES / 1024;
-  static constexpr int UPW = (UNITS + NW - 1) / NW;
-  static constexpr int K_RPU = 1024 / KROW;      // rows per unit
+  static constexpr int BUF = KBYTES + VBYTES;    // one ring slot: K tile then V tile
+  static constexpr int KUNITS = KBYTES / 1024;   // 1 KiB direct-to-LDS copies
+  static constexpr int VUNITS = VBYTES / 1024;
+  static constexpr int KUPW = (KUNITS + NW - 1) / NW;  // copies per wavefront
+  static constexpr int VUPW = (VUNITS + NW - 1) / NW;
+  static constexpr int DMA = KUPW + VUPW;
+  static constexpr int K_RPU = 1024 / KROW;      // rows per copy
   static constexpr int V_RPU = 1024 / VROW;
-  static constexpr int MERGE_WAVE = NDT * 16 * 64 + 128;  // floats
-  static constexpr int MERGE = NRG * MERGE_WAVE * 4;     // bytes
-  static constexpr int SMEM = 2 * BUF > MERGE ? 2 * BUF : MERGE;
-  static_assert(KBYTES % 1024 == 0 && VBYTES % 1024 == 0, "tile is not whole 1 KiB units");
+  static constexpr int MW = NDT * 16 * 64 + 128; // floats of one row group's merge partial
+  static constexpr int MPER = (NRG + STAGES - 1) / STAGES;  // partials per slot
+  static constexpr bool MERGE_IN_SLOTS = MPER * MW * 4 <= BUF;
+  // the vmcnt accounting of a 3-deep ring needs the same copy count on every wavefront
+  static_assert(STAGES == 2 || (KUNITS % NW == 0 && VUNITS % NW == 0), "uneven copies");
   static_assert(QSTEPS * 2 == CPR_K, "K chunk layout");
+  static_assert(STAGES == 2 || STAGES == 3, "ring depth");
 };
 
-template <bool INT8, int D, int BM, int BN>
+template <bool INT8, int D, int BM, int BN, int STAGES>
 __global__ void __launch_bounds__(BM * 4)  // == AttnCfg::NT
 sparse_attn_kernel(AttnArgs a) {
-  using C = AttnCfg<INT8, D, BM, BN>;
+  using C = AttnCfg<INT8, D, BM, BN, STAGES>;
   typedef typename std::conditional<INT8, v4i, v8bf>::type OpT;
   typedef typename std::conditional<INT8, v16i, v16f>::type AccT;
-  __shared__ __attribute__((aligned(1024))) char smem[C::SMEM];
+  // Ring slots are separate arrays and the loop is unrolled over them, so
+  // the compiler can prove that reads of slot j do not alias the copies in
+  // flight into the other slots (it would otherwise drain them first).
+  __shared__ __attribute__((aligned(1024))) char s_0[C::BUF + 256];
+  __shared__ __attribute__((aligned(1024))) char s_1[C::BUF + 256];
+  __shared__ __attribute__((aligned(1024))) char s_2[STAGES > 2 ? C::BUF + 256 : 16];
+  __shared__ __attribute__((aligned(16))) char s_m[C::MERGE_IN_SLOTS ? 16 : C::NRG * C::MW * 4];
 
   const int64_t work = xcd_remap(blockIdx.x, a.n_work);
   if (work < 0) return;
@@ -136,6 +185,9 @@ sparse_attn_kernel(AttnArgs a) {
     }
   }
   const float qs = INT8 ? a.q_scale[bh * a.q_scale_stride + qb] : 1.0f;
+  // Q must be resident before the ring starts: otherwise its pending loads
+  // meet the loop's back edge and the compiler drains at the first MFMA
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   v16f o_acc[C::NDT];
 #pragma unroll
@@ -153,89 +205,101 @@ sparse_attn_kernel(AttnArgs a) {
   const int64_t klast = a.k_len - 1;
   const int64_t krow_bytes = a.skn * C::KB, vrow_bytes = a.svn * 2;
 
-  // Direct-to-LDS staging geometry.  Unit u (1 KiB) of a buffer holds K rows
-  // (u < KUNITS) or V rows; lane l lands at byte l*16 of its unit, so it
-  // loads the swizzled global chunk that belongs there.  Per unit: the tile
-  // row this lane copies and that row's in-row byte offset (32-bit: the host
-  // bounds one head's K/V below 2 GiB).
-  int st_row[C::UPW];
-  int st_col[C::UPW];
+  // Direct-to-LDS staging: copy u of a K (V) tile holds K_RPU (V_RPU) rows;
+  // lane l lands at byte l*16 of it, so it loads the swizzled global chunk
+  // that belongs there.  A block's source address is a uniform 64-bit base
+  // plus a loop-invariant 32-bit lane offset.
+  auto k_row = [&](int i) __attribute__((always_inline)) { return (wave * C::KUPW + i) * C::K_RPU + lane / C::CPR_K; };
+  auto v_row = [&](int i) __attribute__((always_inline)) { return (wave * C::VUPW + i) * C::V_RPU + lane / C::CPR_V; };
+  auto k_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_K) ^ (swz_k(k_row(i)) & (C::CPR_K - 1))) * 16; };
+  auto v_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_V) ^ (swz_v(v_row(i)) & (C::CPR_V - 1))) * 16; };
+  uint32_t k_lo[C::KUPW], v_lo[C::VUPW];
 #pragma unroll
-  for (int i = 0; i < C::UPW; ++i) {
-    const int u = wave * C::UPW + i;
-    if (u < C::KUNITS) {
-      st_row[i] = u * C::K_RPU + lane / C::CPR_K;
-      st_col[i] = ((lane % C::CPR_K) ^ (swz_k(st_row[i]) & (C::CPR_K - 1))) * 16;
-    } else {
-      st_row[i] = (u - C::KUNITS) * C::V_RPU + lane / C::CPR_V;
-      st_col[i] = ((lane % C::CPR_V) ^ (swz_v(st_row[i]) & (C::CPR_V - 1))) * 16;
-    }
-  }
-  // Rows past k_len re-read the last row (those keys are masked).
-  auto stage = [&](int64_t n, int buf) {
-    const int64_t key0 = n * BN;
+  for (int i = 0; i < C::KUPW; ++i)
+    k_lo[i] = static_cast<uint32_t>(k_row(i) * krow_bytes) + k_col(i);
+#pragma unroll
+  for (int i = 0; i < C::VUPW; ++i)
+    v_lo[i] = static_cast<uint32_t>(v_row(i) * vrow_bytes) + v_col(i);
+  // Copy block n (clamped to 0 when invalid) into a slot.  Rows past k_len
+  // re-read the last row (those keys are masked).  (Named source pointers:
+  // an inline pointer expression as this builtin's source argument makes the
+  // host pass drop the kernel stub.)
+  auto stage = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+    const int64_t key0 = (n < 0 ? 0 : n) * BN;
     const bool tail = key0 + BN > a.k_len;
-    char* dst = smem + buf * C::BUF;
+    const char* kb0 = kbase + key0 * krow_bytes;
+    const char* vb0 = vbase + key0 * vrow_bytes;
 #pragma unroll
-    for (int i = 0; i < C::UPW; ++i) {
-      const int u = wave * C::UPW + i;
-      if (u < C::UNITS) {
-        int64_t key = key0 + st_row[i];
-        if (tail) key = min(key, klast);
-        const char* src = u < C::KUNITS
-            ? kbase + static_cast<uint32_t>(key * krow_bytes + st_col[i])
-            : vbase + static_cast<uint32_t>(key * vrow_bytes + st_col[i]);
-        __builtin_amdgcn_global_load_lds(src, RCSA_LDS(void, dst + u * 1024), 16, 0, 0);
+    for (int i = 0; i < C::KUPW; ++i) {
+      if (wave * C::KUPW + i < C::KUNITS) {  // uniform per wavefront
+        const char* src = tail ? kbase + min(key0 + k_row(i), klast) * krow_bytes + k_col(i)
+                               : kb0 + k_lo[i];
+        __builtin_amdgcn_global_load_lds(
+            src, RCSA_LDS(void, dst + (wave * C::KUPW + i) * 1024), 16, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < C::VUPW; ++i) {
+      if (wave * C::VUPW + i < C::VUNITS) {
+        const char* src = tail ? vbase + min(key0 + v_row(i), klast) * vrow_bytes + v_col(i)
+                               : vb0 + v_lo[i];
+        __builtin_amdgcn_global_load_lds(
+            src, RCSA_LDS(void, dst + C::KBYTES + (wave * C::VUPW + i) * 1024), 16, 0, 0);
       }
     }
   };
-  auto block_of = [&](int64_t it) -> int64_t {
-    const int64_t n = list[it];
-    return (n >= 0 && n < a.n_kblocks) ? n : 0;
+  // Block-list entry `it` (-1 = invalid), a scalar load.
+  auto block_of = [&](int64_t it) __attribute__((always_inline)) -> int64_t {
+    const int64_t n = ld_const(list + it);
+    return (n >= 0 && n < a.n_kblocks) ? n : -1;
+  };
+  auto fetch_scale = [&](int64_t n) __attribute__((always_inline)) -> float {
+    return INT8 ? ld_const(a.k_scale + bh * a.k_scale_stride + (n < 0 ? 0 : n)) : 1.0f;
+  };
+  // The BN validity bytes of a whole block ride along with its copies (BN/16
+  // lanes of wavefront 0, 16 bytes each) into the slot's 256-byte tail;
+  // K_valid is 16-byte aligned and readable up to the next 16-byte boundary.
+  auto stage_valid = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+    if (a.kvalid != nullptr && wave == 0 && lane < BN / 16) {
+      const int64_t key0 = (n < 0 ? 0 : n) * BN;
+      const int64_t chunk = min(key0 + 16 * lane, (klast / 16) * 16);
+      const char* src = reinterpret_cast<const char*>(a.kvalid) + chunk;
+      __builtin_amdgcn_global_load_lds(src, RCSA_LDS(void, dst + C::BUF), 16, 0, 0);
+    }
+  };
+  // validity of this lane's key in the wavefront's half, from the slot tail
+  auto key_valid = [&](int64_t n, const char* tile) __attribute__((always_inline)) -> bool {
+    const int64_t key = n * BN + kh * C::HK + lane;
+    if (n < 0 || lane >= C::HK || key >= a.k_len) return false;
+    return a.kvalid == nullptr || tile[C::BUF + kh * C::HK + lane] != 0;
   };
 
   // Lane-dependent LDS read offsets.  The swizzles only involve lane bits,
   // so tile/step offsets (32t, 8u, 4q rows) become instruction immediates.
   int k_off[C::QSTEPS];
   {
-    const int row = key_perm(lr);  // + kh*HK + 32t: multiples of 32
+    const int row = kh * C::HK + key_perm(lr);  // + 32t
     const int sw = swz_k(row) & (C::CPR_K - 1);
 #pragma unroll
     for (int st = 0; st < C::QSTEPS; ++st)
-      k_off[st] = (kh * C::HK + row) * C::KROW + (((hf * C::QSTEPS + st) ^ sw) * 16);
+      k_off[st] = row * C::KROW + (((hf * C::QSTEPS + st) ^ sw) * 16);
   }
   int v_off[C::NDT];
   {
     const int grp = lane >> 4, gi = lane & 15;
-    const int row = 16 * (grp >> 1) + (gi >> 2);  // + kh*HK + 32t + 8u + 4q: multiples of 4
+    const int row = kh * C::HK + 16 * (grp >> 1) + (gi >> 2);  // + 32t + 8u + 4q
     const int sw = swz_v(row) & (C::CPR_V - 1);
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt) {
       const int d = 32 * dt + 16 * (grp & 1) + 4 * (gi & 3);
-      v_off[dt] = C::KBYTES + (kh * C::HK + row) * C::VROW + (((d >> 3) ^ sw) * 16) + (d & 7) * 2;
+      v_off[dt] = C::KBYTES + row * C::VROW + (((d >> 3) ^ sw) * 16) + (d & 7) * 2;
     }
   }
 
-  if (cnt > 0) stage(block_of(0), 0);
-
-  for (int64_t it = 0; it < cnt; ++it) {
-    const int64_t n_raw = list[it];
-    const bool blk_ok = n_raw >= 0 && n_raw < a.n_kblocks;
-    const int64_t n = blk_ok ? n_raw : 0;
-    const int buf = static_cast<int>(it & 1);
-    __syncthreads();  // block `it` is in LDS; everyone is done with the other buffer
-    if (it + 1 < cnt) stage(block_of(it + 1), buf ^ 1);
-
-    const char* tile = smem + buf * C::BUF;
-    const int64_t key0 = n * BN + kh * C::HK;
-
-    // validity of this wavefront's HK keys as a uniform bitmask
-    const int64_t mykey = key0 + lane;
-    const bool kok = blk_ok && lane < C::HK && mykey < a.k_len &&
-                     (a.kvalid == nullptr || a.kvalid[mykey] != 0);
-    const uint64_t vmask = __ballot(kok);
-    const bool all_valid = vmask == (C::HK == 64 ? ~0ull : ((1ull << C::HK) - 1ull));
-
+  // One key block from the slot at `tile`.
+  auto compute = [&](const char* tile, int64_t n, float kscale) __attribute__((always_inline)) {
+    const uint64_t vmask = __ballot(key_valid(n, tile));
+    const bool all_valid = vmask == (~0ull >> (64 - C::HK));
     // ---- S^T = K Q^T ----
     AccT s_acc[C::KT];
 #pragma unroll
@@ -256,7 +320,6 @@ sparse_attn_kernel(AttnArgs a) {
         }
       }
     }
-
     // ---- online softmax: lane half hf, register r <-> key 32t + 16hf + r ----
     // raw value: int8 -> 1.5*2^23 + x read as fp32; bf16 -> the fp32 logit.
     // A masked key's raw value becomes -inf, so max and exp2 need no mask.
@@ -269,8 +332,7 @@ sparse_attn_kernel(AttnArgs a) {
         else rv[t][r] = s_acc[t][r];
       }
     if (!all_valid) {
-      // this lane's 16 keys of each tile as one 32-bit word
-      uint32_t bits = 0;
+      uint32_t bits = 0;  // this lane's 16 keys of each tile as one word
 #pragma unroll
       for (int t = 0; t < C::KT; ++t)
         bits |= static_cast<uint32_t>((vmask >> (32 * t + 16 * hf)) & 0xffffull) << (16 * t);
@@ -285,11 +347,11 @@ sparse_attn_kernel(AttnArgs a) {
     for (int t = 0; t < C::KT; ++t)
 #pragma unroll
       for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, rv[t][r]);
-    rmax = fmaxf(rmax, __shfl_xor(rmax, 32, kWave));
-    const float c = INT8 ? a.scale_log2 * qs * a.k_scale[bh * a.k_scale_stride + n]
-                         : a.scale_log2;
+    rmax = pair_max(rmax);  // with the partner lane (lane ^ 32)
+    const float c = INT8 ? a.scale_log2 * qs * kscale : a.scale_log2;
     const float m_blk = (rmax == -INFINITY) ? -INFINITY
                         : (INT8 ? (rmax - kMagicF) * c : rmax * c);
+    // lazy rescale: move the running max only when it grows by > 2^kTau
     if (__ballot(m_blk > m_run + kTau) != 0) {  // wavefront-uniform
       const float m_new = fmaxf(m_run, m_blk);
       const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
@@ -301,25 +363,22 @@ sparse_attn_kernel(AttnArgs a) {
       m_run = m_new;
     }
     const float bias = -(INT8 ? c * kMagicF : 0.0f) - (m_run == -INFINITY ? 0.0f : m_run);
-
     v8bf p_op[C::KT][2];
 #pragma unroll
     for (int t = 0; t < C::KT; ++t)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + j], c, bias));
-          p_op[t][u][j] = static_cast<__bf16>(e);
-        }
+        for (int jj = 0; jj < 8; ++jj)
+          p_op[t][u][jj] =
+              static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + jj], c, bias)));
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const v2bf pair = {p_op[t][u][2 * j], p_op[t][u][2 * j + 1]};
+        for (int jj = 0; jj < 4; ++jj) {
+          const v2bf pair = {p_op[t][u][2 * jj], p_op[t][u][2 * jj + 1]};
           const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
           l_run = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_run, false);
         }
       }
-
     // ---- O^T += V^T P^T, V^T operand by transposing LDS reads ----
 #pragma unroll
     for (int t = 0; t < C::KT; ++t)
@@ -329,18 +388,74 @@ sparse_attn_kernel(AttnArgs a) {
         for (int dt = 0; dt < C::NDT; ++dt) {
           const char* p0 = tile + v_off[dt] + (32 * t + 8 * u) * C::VROW;
           const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0));
-          const v4bf hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-              RCSA_LDS(v4bf, p0 + 4 * C::VROW));
+          const v4bf hi =
+              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0 + 4 * C::VROW));
           const v8bf v_op = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
           o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_op, p_op[t][u], o_acc[dt],
                                                              0, 0, 0);
         }
+  };
+
+  // ---- ring: block j lives in slot j % STAGES; STAGES-1 blocks in flight ----
+  // List entries are read one iteration before they are staged (scalar
+  // loads whose latency hides behind that iteration's compute).
+  int64_t n_m[3] = {-1, -1, -1};
+  float ks_m[3] = {1.0f, 1.0f, 1.0f};
+#pragma unroll
+  for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
+    if (sidx < cnt) {
+      char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
+      n_m[sidx] = block_of(sidx);
+      ks_m[sidx] = fetch_scale(n_m[sidx]);
+      stage_valid(n_m[sidx], dst);
+      stage(n_m[sidx], dst);
+    }
+  }
+  int64_t n_pre = STAGES - 1 < cnt ? block_of(STAGES - 1) : -1;  // next block to stage
+  auto iteration = [&](auto slot_c, int64_t j) __attribute__((always_inline)) {
+    constexpr int J = decltype(slot_c)::value;
+    constexpr int F = (J + STAGES - 1) % STAGES;  // slot of block j + STAGES - 1
+    char* const tile = J == 0 ? s_0 : J == 1 ? s_1 : s_2;
+    char* const fill = F == 0 ? s_0 : F == 1 ? s_1 : s_2;
+    // block j's copies are the oldest in flight; the STAGES-2 younger
+    // stages may remain (wavefront 0's extra validity copy is waited too),
+    // then every wavefront's copies of block j have landed and slot F is free
+    if constexpr (STAGES == 3) {
+      if (j + 1 < cnt) wait_vm_barrier<C::DMA>();
+      else wait_vm_barrier<0>();
+    } else {
+      wait_vm_barrier<0>();
+    }
+    if (j + STAGES - 1 < cnt) {
+      n_m[F] = n_pre;
+      ks_m[F] = fetch_scale(n_pre);
+      stage_valid(n_pre, fill);
+      stage(n_pre, fill);
+      n_pre = j + STAGES < cnt ? block_of(j + STAGES) : -1;
+    }
+    compute(tile, n_m[J], ks_m[J]);
+  };
+  for (int64_t j = 0; j < cnt; j += STAGES) {
+    iteration(std::integral_constant<int, 0>{}, j);
+    if (j + 1 >= cnt) break;
+    iteration(std::integral_constant<int, 1>{}, j + 1);
+    if constexpr (STAGES > 2) {
+      if (j + 2 >= cnt) break;
+      iteration(std::integral_constant<int, 2>{}, j + 2);
+    }
   }
 
   // ---- merge the two key halves, normalise, write O (bf16) and the LSE ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32, kWave);
+  const float l_tot = pair_sum(l_run);
   __syncthreads();  // main loop done everywhere: LDS is free for the merge
-  float* mbuf = reinterpret_cast<float*>(smem) + rg * C::MERGE_WAVE;
+  float* mbuf;
+  if constexpr (C::MERGE_IN_SLOTS) {
+    const int sl = rg % STAGES;
+    mbuf = reinterpret_cast<float*>(sl == 0 ? s_0 : sl == 1 ? s_1 : s_2) +
+           (rg / STAGES) * C::MW;
+  } else {
+    mbuf = reinterpret_cast<float*>(s_m) + rg * C::MW;
+  }
   if (kh == 1) {
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
@@ -367,9 +482,9 @@ sparse_attn_kernel(AttnArgs a) {
         for (int g = 0; g < 4; ++g) {
           float o4[4];
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * g + j;
-            o4[j] = o_acc[dt][r] * fa + mbuf[(dt * 16 + r) * 64 + lane] * fb;
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            o4[e] = o_acc[dt][r] * fa + mbuf[(dt * 16 + r) * 64 + lane] * fb;
           }
           const int d0 = 32 * dt + 8 * g + 4 * hf;
           *reinterpret_cast<uint2*>(op + d0) =
@@ -385,20 +500,21 @@ sparse_attn_kernel(AttnArgs a) {
 template <bool INT8>
 static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
   const dim3 grid(static_cast<unsigned>(xcd_grid(a.n_work)));
-#define RCSA_ATTN(D_, BM_, BN_)                                                   \
-  if (D == D_ && BM == BM_ && BN == BN_) {                                        \
-    sparse_attn_kernel<INT8, D_, BM_, BN_>                                        \
-        <<<grid, dim3(AttnCfg<INT8, D_, BM_, BN_>::NT), 0, s>>>(a);               \
-    return launch_status();                                                       \
+  // int8 at D=128, 128x128 blocks keeps two blocks in flight (3 x 48 KiB);
+  // the other shapes double-buffer.
+#define RCSA_ATTN(D_, BM_, BN_, ST_)                                               \
+  if (D == D_ && BM == BM_ && BN == BN_) {                                          \
+    sparse_attn_kernel<INT8, D_, BM_, BN_, ST_><<<grid, dim3(BM_ * 4), 0, s>>>(a);   \
+    return launch_status();                                                         \
   }
-  RCSA_ATTN(128, 128, 128)
-  RCSA_ATTN(128, 128, 64)
-  RCSA_ATTN(128, 64, 128)
-  RCSA_ATTN(128, 64, 64)
-  RCSA_ATTN(64, 128, 128)
-  RCSA_ATTN(64, 128, 64)
-  RCSA_ATTN(64, 64, 128)
-  RCSA_ATTN(64, 64, 64)
+  RCSA_ATTN(128, 128, 128, INT8 ? 3 : 2)
+  RCSA_ATTN(128, 128, 64, 2)
+  RCSA_ATTN(128, 64, 128, 2)
+  RCSA_ATTN(128, 64, 64, 2)
+  RCSA_ATTN(64, 128, 128, 2)
+  RCSA_ATTN(64, 128, 64, 2)
+  RCSA_ATTN(64, 64, 128, 2)
+  RCSA_ATTN(64, 64, 64, 2)
 #undef RCSA_ATTN
   return RCSA_ERR_SHAPE;
 }
