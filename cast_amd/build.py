@@ -52,7 +52,8 @@ def _compile(src: Path, obj: Path) -> None:
         raise RuntimeError(f"hipcc failed for {src.name}:\n" + "\n".join(lines))
     _check_resources(src, lines)
     other = [line for line in lines if "remark:" not in line and line.strip()
-             and not line.lstrip().startswith(("|", "^")) and not line[:1].isdigit()]
+             and not line.lstrip().startswith(("|", "^"))
+             and not line.lstrip()[:1].isdigit()]
     if other:
         print("\n".join(other), file=sys.stderr)
     _check_stubs(obj)

@@ -538,6 +538,9 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   if (svn % 8 || svh % 8 || svz % 8) return RCSA_ERR_STRIDE;
   if (som % 4 || soh % 4 || soz % 4) return RCSA_ERR_STRIDE;
   if (reinterpret_cast<uintptr_t>(Out) & 7u) return RCSA_ERR_ALIGN;
+  // validity bytes are copied in aligned 16-byte chunks (the chunk holding the
+  // last byte stays inside the same page, so no padding is needed)
+  if (reinterpret_cast<uintptr_t>(K_valid) & 15u) return RCSA_ERR_ALIGN;
   a.kvalid = K_valid;
   a.scale_log2 = sm_scale * 1.4426950408889634f;
   a.lse = M;

@@ -58,7 +58,10 @@ def _valid_u8(valid: Optional[torch.Tensor], n: int, device, fn: str) -> Optiona
     v = valid.reshape(-1)
     if v.numel() != n:
         raise ValueError(f"{fn}: valid mask has {v.numel()} entries, expected {n}")
-    return _bytes_mask(v, device)
+    v = _bytes_mask(v, device)
+    if v.data_ptr() % 16:  # an offset view; the kernels read 16-byte chunks
+        v = v.clone()
+    return v
 
 
 def _bhld(x: torch.Tensor, block_size: int, fn: str) -> tuple[int, int, int, int, int]:

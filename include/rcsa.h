@@ -152,6 +152,9 @@ int rcsa_quantize_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
  * Indices outside [0, ceil(K_LEN/BLOCK_N)) are skipped; lens are clamped to
  * [0, max_k].  Strides are in elements; every *_k / *_bs stride must be 1.
  * HEAD_DIM in {64, 128}; BLOCK_M, BLOCK_N in {64, 128}.
+ * Alignment: Q/K/V rows 16-byte aligned, Out 8-byte aligned, K_valid (when
+ * not NULL) 16-byte aligned -- it is read in aligned 16-byte chunks, so up
+ * to 15 bytes past K_LEN inside the same chunk may be read (never used).
  */
 int rcsa_sparse_attn_bf16(const void* Q, const void* K, const void* V,
                           const uint8_t* K_valid, float sm_scale, float* M,

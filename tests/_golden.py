@@ -1,0 +1,52 @@
+"""Loading of the committed golden fixtures and of the workloads they were
+made from (shared by the CPU and GPU golden tests)."""
+import functools
+import hashlib
+from pathlib import Path
+
+import numpy as np
+import torch
+
+from cast_amd import workloads
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+ATTN_QBLOCKS = (0, 27)
+
+
+def load(name: str) -> dict:
+    with np.load(GOLDEN / f"{name}.npz", allow_pickle=False) as f:
+        return {k: f[k] for k in f.files}
+
+
+def fingerprint(w) -> str:
+    h = hashlib.sha256()
+    for t in (w.q, w.k, w.v, w.q_valid, w.k_valid, w.forced):
+        t = t.detach().cpu().contiguous()
+        if t.dtype == torch.bfloat16:
+            t = t.view(torch.int16)
+        h.update(t.numpy().tobytes())
+    return h.hexdigest()
+
+
+@functools.lru_cache(maxsize=None)
+def workload(name: str):
+    """The seeded workload behind a fixture (CPU tensors, cached per process)."""
+    if name == "c0_plumbing":
+        return workloads.plumbing(0)
+    if name == "c1_dit_bf16":
+        return workloads.matrix_dit(0)
+    if name == "c2_dit_int8":
+        return workloads.matrix_dit(0, int8=True)
+    if name == "c3_selection":
+        return workloads.selection_stress(0)
+    raise KeyError(name)
+
+
+def set_equal_where(idx_a, cnt_a, idx_b, cnt_b, rows_mask) -> int:
+    """Number of rows in ``rows_mask`` whose selected sets differ."""
+    bad = 0
+    for r, i in zip(*np.nonzero(rows_mask)):
+        ca, cb = int(cnt_a[r, i]), int(cnt_b[r, i])
+        if ca != cb or set(idx_a[r, i, :ca].tolist()) != set(idx_b[r, i, :cb].tolist()):
+            bad += 1
+    return bad

@@ -1,0 +1,505 @@
+"""Pins for the CPU oracle (oracle/rcsa_oracle.py).
+
+The reference ships no golden vectors or known-answer tests for this path,
+so each oracle function is checked here against something the mathematics
+fixes independently of the oracle's own formula: fp64 brute-force loops,
+closed forms, invariants, and textbook library routines.  The
+``test_planted_*`` cases plant a plausible mistake in a copy of an oracle
+function and show that the pin catches it.
+"""
+import math
+import random
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import rcsa_oracle as orc
+
+
+def _rand(shape, seed, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=dtype)
+
+
+# ---------------------------------------------------------------- pooling
+
+def _pool_brute(x, valid, bs):
+    """fp64 triple loop: masked mean over valid tokens, then x / max(|x|, 1e-12)."""
+    B, H, L, D = x.shape
+    nb = L // bs
+    out = np.zeros((B, H, nb, D))
+    xn = x.double().numpy()
+    vn = np.ones(L, bool) if valid is None else valid.numpy().astype(bool)
+    for b in range(B):
+        for h in range(H):
+            for n in range(nb):
+                acc = np.zeros(D)
+                cnt = 0
+                for t in range(n * bs, (n + 1) * bs):
+                    if vn[t]:
+                        acc += xn[b, h, t]
+                        cnt += 1
+                mean = acc / max(cnt, 1)
+                out[b, h, n] = mean / max(math.sqrt(float((mean * mean).sum())), 1e-12)
+    return out
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_pool_blocks_brute_force(masked):
+    x = _rand((1, 2, 6 * 16, 8), 1)
+    valid = None
+    if masked:
+        valid = torch.rand(96, generator=torch.Generator().manual_seed(2)) > 0.3
+        valid[16:32] = False  # one empty block
+    hat, sums, nvalid = orc.pool_blocks(x, valid, 16)
+    ref = _pool_brute(x, valid, 16)
+    np.testing.assert_allclose(hat.numpy(), ref, rtol=1e-5, atol=1e-6)
+    if masked:
+        assert float(nvalid[1]) == 0
+        assert torch.all(hat[:, :, 1] == 0)
+
+
+def test_pool_blocks_closed_forms():
+    # a block whose tokens are all equal to c pools to c/|c|; an all-zero block to 0
+    D = 8
+    c = torch.arange(1, D + 1, dtype=torch.float32)
+    x = torch.zeros(1, 1, 32, D)
+    x[0, 0, :16] = c
+    hat, _, _ = orc.pool_blocks(x, None, 16)
+    torch.testing.assert_close(hat[0, 0, 0], c / c.norm())
+    assert torch.all(hat[0, 0, 1] == 0)
+    # invalid tokens do not move the mean
+    y = x.clone()
+    y[0, 0, 8:16] = 1e6
+    valid = torch.ones(32, dtype=torch.bool)
+    valid[8:16] = False
+    hat2, _, n = orc.pool_blocks(y, valid, 16)
+    torch.testing.assert_close(hat2[0, 0, 0], c / c.norm())
+    assert n.tolist() == [8.0, 16.0]
+
+
+# ---------------------------------------------------------------- scores
+
+def test_block_scores_brute_force_and_bounds():
+    q = F.normalize(_rand((2, 5, 16), 3), dim=-1)
+    k = F.normalize(_rand((2, 7, 16), 4), dim=-1)
+    s = orc.block_scores(q, k)
+    qn, kn = q.double().numpy(), k.double().numpy()
+    ref = np.array([[[sum(qn[b, i, d] * kn[b, j, d] for d in range(16)) for j in range(7)]
+                     for i in range(5)] for b in range(2)])
+    np.testing.assert_allclose(s.numpy(), ref, rtol=1e-5, atol=1e-6)
+    assert float(s.abs().max()) <= 1 + 1e-6  # Cauchy-Schwarz on unit vectors
+    self_s = orc.block_scores(q, q)
+    torch.testing.assert_close(torch.diagonal(self_s, dim1=-2, dim2=-1),
+                               torch.ones(2, 5), atol=1e-6, rtol=0)
+
+
+# ---------------------------------------------------------------- stencil
+
+def test_local_stencil_loop():
+    nt, nh, nw = 3, 2, 4
+    n = nt * nh * nw
+    m = orc.local_stencil(n, nh, nw)
+    for a in range(n):
+        ta, ha, wa = a // (nh * nw), (a // nw) % nh, a % nw
+        for b in range(n):
+            tb, hb, wb = b // (nh * nw), (b // nw) % nh, b % nw
+            assert bool(m[a, b]) == (abs(ta - tb) + abs(ha - hb) + abs(wa - wb) <= 1)
+    assert torch.equal(m, m.T)
+    assert int(m.sum(1).max()) <= 7
+
+
+# ---------------------------------------------------------------- top-k
+
+def _select_brute(score, k, forced, allowed, order):
+    """Python sort with tuple keys: allowed first, then forced, score desc (NaN as
+    +inf, -0 as +0), index asc; keep min(k, n_allowed); index or rank order."""
+    nbh, nq, nk = score.shape
+    idx, cnt = [], []
+    for r in range(nbh):
+        ri, rc = [], []
+        for i in range(nq):
+            cols = []
+            for j in range(nk):
+                s = float(score[r, i, j])
+                if math.isnan(s):
+                    s = math.inf
+                if s == 0:
+                    s = 0.0
+                a = True if allowed is None else bool(allowed[r, i, j])
+                f = False if forced is None else bool(forced[r, i, j])
+                cols.append((not a, not f, -s, j))
+            cols.sort()
+            kk = k if isinstance(k, int) else int(k[r, i])
+            n_allowed = sum(1 for c in cols if not c[0])
+            c = min(kk, n_allowed)
+            sel = [t[3] for t in cols[:c]]
+            if order == "index":
+                sel.sort()
+            ri.append(sel)
+            rc.append(c)
+        idx.append(ri)
+        cnt.append(rc)
+    return idx, cnt
+
+
+def _tie_heavy_scores(nbh, nq, nk, seed):
+    g = torch.Generator().manual_seed(seed)
+    s = torch.randint(-4, 5, (nbh, nq, nk), generator=g).float() / 4  # many exact ties
+    s[0, 0, :3] = torch.tensor([0.0, -0.0, float("nan")])
+    return s
+
+
+@pytest.mark.parametrize("order", ["index", "rank"])
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_select_topk_brute_force(order, seed):
+    nbh, nq, nk = 3, 5, 23
+    s = _tie_heavy_scores(nbh, nq, nk, seed)
+    g = torch.Generator().manual_seed(100 + seed)
+    forced = torch.rand(nbh, nq, nk, generator=g) < 0.15
+    allowed = torch.rand(nbh, nq, nk, generator=g) < 0.8
+    allowed[1, 2] = False  # a row with nothing allowed
+    allowed[2, 3, :] = False
+    allowed[2, 3, :4] = True  # a row with fewer allowed than k
+    k = torch.randint(0, 12, (nbh, nq), generator=g)
+    idx, cnt = orc.select_topk(s, k, forced=forced, allowed=allowed, max_k=12, order=order)
+    bi, bc = _select_brute(s, k, forced, allowed, order)
+    for r in range(nbh):
+        for i in range(nq):
+            c = bc[r][i]
+            assert int(cnt[r, i]) == c
+            assert idx[r, i, :c].tolist() == bi[r][i]
+            assert torch.all(idx[r, i, c:] == -1)
+
+
+def test_select_topk_invariants():
+    nbh, nq, nk = 2, 6, 40
+    s = _rand((nbh, nq, nk), 7)
+    forced = torch.zeros(nq, nk, dtype=torch.bool)
+    forced[:, ::8] = True  # 5 forced per row, as an anchor interval of 8
+    forced_scores = s.clone()
+    forced_scores[:, :, ::8] = -10.0  # forced columns carry the lowest scores
+    idx, cnt = orc.select_topk(forced_scores, 9, forced=forced)
+    for r in range(nbh):
+        for i in range(nq):
+            sel = set(idx[r, i, :9].tolist())
+            assert set(range(0, nk, 8)) <= sel          # every forced block kept
+            rest = sorted(sel - set(range(0, nk, 8)))
+            free = [j for j in range(nk) if j % 8]
+            best = sorted(free, key=lambda j: (-float(s[r, i, j]), j))[:4]
+            assert rest == sorted(best)                 # then the best 4 by score
+    assert torch.all(cnt == 9)
+
+
+def test_topk_margin_brute_force():
+    s = _rand((2, 4, 15), 9)
+    forced = torch.zeros(4, 15, dtype=torch.bool)
+    forced[0, :3] = True
+    m = orc.topk_margin(s, 5, forced=forced)
+    for r in range(2):
+        for i in range(4):
+            f = [bool(forced[i, j]) for j in range(15)]
+            cols = sorted(range(15), key=lambda j: (not f[j], -float(s[r, i, j]), j))
+            a, b = cols[4], cols[5]
+            want = math.inf if f[a] != f[b] else float(s[r, i, a] - s[r, i, b])
+            assert float(m[r, i]) == pytest.approx(want, rel=1e-6)
+
+
+def test_planted_tie_order_is_caught():
+    """Ties broken towards the higher index (a plausible slip) disagree with the
+    brute-force rule on tie-heavy scores."""
+    s = _tie_heavy_scores(2, 4, 19, 5)
+    flipped = torch.flip(s, dims=[-1])
+    idx_f, cnt = orc.select_topk(flipped, 6, order="rank")
+    wrong = (18 - idx_f).clamp(max=18)  # index map back: ties now prefer high index
+    bi, _ = _select_brute(s, 6, None, None, "rank")
+    mismatched = any(wrong[r, i, :6].tolist() != bi[r][i] for r in range(2) for i in range(4))
+    assert mismatched
+
+
+# ---------------------------------------------------------------- quantiser
+
+def test_quantize_query_error_bound_and_range():
+    q = _rand((1, 2, 64, 16), 11) * 3
+    valid = torch.ones(64, dtype=torch.bool)
+    valid[40:] = False
+    q8, scale = orc.quantize_query_blocks(q, valid, 32)
+    deq = orc.dequantize_blocks(q8, scale, 32)
+    x = q.reshape(1, 2, 2, 32, 16)
+    err = (deq.reshape(1, 2, 2, 32, 16) - x).abs()
+    sc = scale.reshape(1, 2, 2, 1, 1)
+    vm = valid.reshape(2, 32)[None, None, :, :, None]
+    assert torch.all(torch.where(vm, err, torch.zeros_like(err)) <= sc / 2 * (1 + 1e-6))
+    assert int(q8.abs().max()) == 127
+    assert torch.all(q8.reshape(1, 2, 64, 16)[:, :, 40:] == 0)
+    # the block's largest |q| lands exactly on +-127
+    for h in range(2):
+        for n in range(2):
+            blk = x[0, h, n][vm[0, 0, n, :, 0]]
+            amax = float(blk.abs().max())
+            assert float(scale[h, n]) == pytest.approx(amax / 127, rel=1e-7)
+
+
+def test_quantize_idempotent_and_zero_block():
+    q = _rand((1, 1, 64, 16), 12)
+    q[0, 0, 32:] = 0
+    q8, scale = orc.quantize_query_blocks(q, None, 32)
+    assert float(scale[0, 1]) == 1.0 and torch.all(q8[0, 0, 32:] == 0)
+    deq = orc.dequantize_blocks(q8, scale, 32)
+    q8b, scale_b = orc.quantize_query_blocks(deq, None, 32)
+    assert torch.equal(q8, q8b)
+    torch.testing.assert_close(scale, scale_b, rtol=1e-6, atol=0)
+
+
+def test_key_mean_and_smoothing_invariance():
+    k = _rand((1, 2, 48, 8), 13, torch.float64)
+    valid = torch.ones(48, dtype=torch.bool)
+    valid[5] = valid[30] = False
+    m = orc.key_mean(k.float(), valid)
+    want = k[0][:, valid].mean(dim=1)
+    torch.testing.assert_close(m.double(), want.reshape(2, 8), rtol=1e-6, atol=1e-7)
+    # softmax(q . (k - m)) == softmax(q . k): the per-head mean shifts every
+    # logit of a query row by the same q . m
+    q = _rand((2, 5, 8), 14, torch.float64)
+    a = torch.softmax(q @ k[0].transpose(-1, -2), dim=-1)
+    b = torch.softmax(q @ (k[0] - m.double()[:, None]).transpose(-1, -2), dim=-1)
+    torch.testing.assert_close(a, b, rtol=1e-12, atol=1e-14)
+
+
+def test_quantize_key_error_bound():
+    k = _rand((1, 2, 64, 16), 15) + 5.0  # a large common offset
+    valid = torch.ones(64, dtype=torch.bool)
+    valid[60:] = False
+    m = orc.key_mean(k, valid)
+    k8, scale = orc.quantize_key_blocks(k, valid, 32, m)
+    deq = orc.dequantize_blocks(k8, scale, 32) + m.reshape(1, 2, 1, 16)
+    err = (deq - k).abs().reshape(1, 2, 2, 32, 16)
+    vm = valid.reshape(2, 32)[None, None, :, :, None]
+    sc = scale.reshape(1, 2, 2, 1, 1)
+    assert torch.all(torch.where(vm, err, torch.zeros_like(err)) <= sc / 2 * (1 + 1e-5))
+    # smoothing shrinks the scale well below the unsmoothed absmax/127
+    assert float(scale.max()) < float(k.abs().max()) / 127 * 0.75
+
+
+# ---------------------------------------------------------------- attention
+
+def _attn_brute(q, k, v, blocks_per_qblock, kvalid, bm, bn, scale):
+    """fp64 per-row loops: explicit max-shifted exp and sums."""
+    B, H, Lq, D = q.shape
+    Lk = k.shape[2]
+    out = np.zeros((B, H, Lq, D))
+    lse = np.full((B, H, Lq), -np.inf)
+    qn, kn, vn = q.double().numpy(), k.double().numpy(), v.double().numpy()
+    for b in range(B):
+        for h in range(H):
+            for r in range(Lq):
+                keys = [t for n in blocks_per_qblock[b][h][r // bm]
+                        for t in range(n * bn, min((n + 1) * bn, Lk)) if kvalid[t]]
+                if not keys:
+                    continue
+                logits = [scale * float(np.dot(qn[b, h, r], kn[b, h, t])) for t in keys]
+                mx = max(logits)
+                w = [math.exp(x - mx) for x in logits]
+                z = sum(w)
+                out[b, h, r] = sum(wi * vn[b, h, t] for wi, t in zip(w, keys)) / z
+                lse[b, h, r] = mx + math.log(z)
+    return out, lse
+
+
+def test_sparse_attention_brute_force():
+    B, H, D, bm, bn = 1, 2, 16, 8, 8
+    Lq, Lk = 20, 44  # ragged: the last query block holds 4 rows, the last key block 4 keys
+    q, k, v = _rand((B, H, Lq, D), 21), _rand((B, H, Lk, D), 22), _rand((B, H, Lk, D), 23)
+    kvalid = torch.rand(Lk, generator=torch.Generator().manual_seed(24)) > 0.2
+    kvalid[8:16] = False  # a fully masked key block
+    nqb = 3
+    idx = torch.full((B, H, nqb, 4), -1, dtype=torch.int32)
+    cnt = torch.zeros(B, H, nqb, dtype=torch.int32)
+    lists = [[[[5, 0, 2], [1], [3, 4, 5, 0]], [[], [1, 2], [4]]]]
+    for h in range(H):
+        for m in range(nqb):
+            L = lists[0][h][m]
+            idx[0, h, m, :len(L)] = torch.tensor(L, dtype=torch.int32)
+            cnt[0, h, m] = len(L)
+    out, lse = orc.sparse_attention(q, k, v, idx, cnt, kvalid, block_m=bm, block_n=bn,
+                                    dtype=torch.float64)
+    ref_o, ref_l = _attn_brute(q, k, v, lists, kvalid.tolist(), bm, bn, 1 / math.sqrt(D))
+    np.testing.assert_allclose(out.numpy(), ref_o, rtol=1e-10, atol=1e-12)
+    np.testing.assert_allclose(lse.numpy(), ref_l, rtol=1e-10, atol=1e-12)
+    # the empty list and the block of masked keys both give 0 output / lse -inf
+    assert torch.all(out[0, 1, :8] == 0) and torch.all(torch.isinf(lse[0, 1, :8]))
+    assert torch.all(out[0, 0, 8:16] == 0)
+
+
+def test_sparse_attention_matches_dense_sdpa():
+    """With every block selected and every key valid the op is textbook attention."""
+    B, H, L, D, bs = 1, 3, 32, 16, 8
+    q, k, v = (_rand((B, H, L, D), s, torch.float64) for s in (31, 32, 33))
+    nb = L // bs
+    idx = torch.arange(nb, dtype=torch.int32).expand(B, H, nb, nb).contiguous()
+    cnt = torch.full((B, H, nb), nb, dtype=torch.int32)
+    out, _ = orc.sparse_attention(q, k, v, idx, cnt, None, block_m=bs, block_n=bs,
+                                  dtype=torch.float64)
+    ref = F.scaled_dot_product_attention(q, k, v)
+    torch.testing.assert_close(out, ref, rtol=1e-10, atol=1e-12)
+
+
+def test_sparse_attention_closed_forms():
+    D, bs = 8, 4
+    q = _rand((1, 1, 4, D), 41)
+    v = _rand((1, 1, 8, D), 42)
+    idx = torch.tensor([[[[1]]]], dtype=torch.int32)
+    cnt = torch.tensor([[[1]]], dtype=torch.int32)
+    # one valid key -> its value row, lse = its logit
+    kvalid = torch.tensor([0, 0, 0, 0, 0, 0, 1, 0], dtype=torch.bool)
+    k = _rand((1, 1, 8, D), 43)
+    out, lse = orc.sparse_attention(q, k, v, idx, cnt, kvalid, block_m=bs, block_n=bs)
+    torch.testing.assert_close(out[0, 0], v[0, 0, 6].expand(4, D))
+    torch.testing.assert_close(lse[0, 0], (q[0, 0] @ k[0, 0, 6]) / math.sqrt(D))
+    # equal logits (zero query) -> the mean of the listed values
+    out0, lse0 = orc.sparse_attention(torch.zeros_like(q), k, v, idx, cnt, None,
+                                      block_m=bs, block_n=bs)
+    torch.testing.assert_close(out0[0, 0], v[0, 0, 4:8].mean(0).expand(4, D))
+    torch.testing.assert_close(lse0[0, 0], torch.full((4,), math.log(4.0)))
+    # index order inside the list does not matter
+    idx2 = torch.tensor([[[[1, 0]]]], dtype=torch.int32)
+    idx3 = torch.tensor([[[[0, 1]]]], dtype=torch.int32)
+    c2 = torch.tensor([[[2]]], dtype=torch.int32)
+    a, _ = orc.sparse_attention(q, k, v, idx2, c2, None, block_m=bs, block_n=bs)
+    b, _ = orc.sparse_attention(q, k, v, idx3, c2, None, block_m=bs, block_n=bs)
+    torch.testing.assert_close(a, b)
+
+
+def test_planted_scale_slip_is_caught():
+    """Forgetting the 1/sqrt(D) factor (a plausible slip) fails the dense pin."""
+    B, H, L, D, bs = 1, 1, 16, 16, 8
+    q, k, v = (_rand((B, H, L, D), s, torch.float64) for s in (51, 52, 53))
+    idx = torch.arange(2, dtype=torch.int32).expand(B, H, 2, 2).contiguous()
+    cnt = torch.full((B, H, 2), 2, dtype=torch.int32)
+    wrong, _ = orc.sparse_attention(q, k, v, idx, cnt, None, block_m=bs, block_n=bs,
+                                    sm_scale=1.0, dtype=torch.float64)
+    ref = F.scaled_dot_product_attention(q, k, v)
+    assert float((wrong - ref).abs().max()) > 1e-3
+
+
+def test_sparse_attention_int8_is_dequantised_attention():
+    B, H, L, D, bs = 1, 1, 16, 8, 8
+    q, k, v = _rand((B, H, L, D), 61), _rand((B, H, L, D), 62), _rand((B, H, L, D), 63)
+    q8, qs = orc.quantize_query_blocks(q, None, bs)
+    m = orc.key_mean(k, None)
+    k8, ks = orc.quantize_key_blocks(k, None, bs, m)
+    idx = torch.arange(2, dtype=torch.int32).expand(B, H, 2, 2).contiguous()
+    cnt = torch.full((B, H, 2), 2, dtype=torch.int32)
+    a, _ = orc.sparse_attention_int8(q8, qs, k8, ks, v, idx, cnt, None, block_m=bs, block_n=bs)
+    b, _ = orc.sparse_attention(orc.dequantize_blocks(q8, qs, bs), orc.dequantize_blocks(k8, ks, bs),
+                                v, idx, cnt, None, block_m=bs, block_n=bs)
+    torch.testing.assert_close(a, b)
+    # and, by smoothing invariance, close to the unquantised result
+    c, _ = orc.sparse_attention(q, k, v, idx, cnt, None, block_m=bs, block_n=bs)
+    assert orc.equivalence_stats(c, a)["cosine"] > 0.999
+
+
+def test_equivalence_stats_closed_forms():
+    r = torch.tensor([3.0, 4.0])
+    s = orc.equivalence_stats(r, r)
+    assert s["cosine"] == pytest.approx(1.0) and s["max_abs"] == 0 and s["relative_l2"] == 0
+    s2 = orc.equivalence_stats(r, torch.tensor([3.0, 5.0]))
+    assert s2["relative_l2"] == pytest.approx(1 / 5, rel=1e-5)
+    assert s2["max_abs"] == 1.0 and s2["mae"] == 0.5
+    assert s2["cosine"] == pytest.approx(29 / (5 * math.sqrt(34)), rel=1e-6)
+
+
+# ---------------------------------------------------------------- layout
+
+def _layout_argsort(active_frames, mem_t, H, W, shape):
+    """Independent formulation: block id per compact token, then a stable argsort."""
+    tt, th, tw = shape
+    frames = sorted(active_frames)
+    ct, spatial = len(frames), H * W
+    nh, nw = -(-H // th), -(-W // tw)
+    cm = sum(1 for f in frames if f < mem_t)
+    tok = np.arange(ct * spatial)
+    lt, ls = tok // spatial, tok % spatial
+    if cm:
+        cells = -(-cm // tt)
+        cell = np.where(lt < cm, lt // tt, cells + (lt - cm) // tt)
+        nb = (cells + -(-(ct - cm) // tt)) * nh * nw
+    else:
+        cell = lt // tt
+        nb = -(-ct // tt) * nh * nw
+    bid = cell * nh * nw + (ls // W // th) * nw + (ls % W) // tw
+    order = np.argsort(bid, kind="stable")
+    return bid, order, nb
+
+
+@pytest.mark.parametrize("frames,mem_t,H,W,shape", [
+    ([0, 1, 2, 3], 0, 8, 8, (2, 4, 4)),
+    ([0, 2, 5, 6, 7], 3, 6, 10, (2, 4, 4)),   # ragged spatial tiles + memory split
+    ([1, 4], 2, 4, 4, (4, 2, 2)),
+])
+def test_compact_layout_vs_argsort(frames, mem_t, H, W, shape):
+    idx, valid, t2p = orc.compact_layout(frames, mem_t, H, W, shape)
+    bid, order, nb = _layout_argsort(frames, mem_t, H, W, shape)
+    assert idx.shape[0] == nb
+    bs = shape[0] * shape[1] * shape[2]
+    flat = idx.reshape(-1)
+    members = flat[flat >= 0].numpy()
+    # grouped by block id, stable inside a block
+    np.testing.assert_array_equal(np.sort(members), np.arange(len(bid)))
+    np.testing.assert_array_equal(bid[members], np.sort(bid[order]))
+    np.testing.assert_array_equal(members, order)
+    # round trip: packed slot of token t holds t
+    np.testing.assert_array_equal(flat[t2p].numpy(), np.arange(len(bid)))
+    assert int(valid.sum()) == len(bid) and valid.shape == (nb, bs)
+
+
+# ---------------------------------------------------------------- budgets
+
+def test_apportion_textbook_and_invariants():
+    assert orc.apportion([0.5, 0.3, 0.2], 10) == [5, 3, 2]
+    assert orc.apportion([1, 1, 1], 10) == [4, 3, 3]       # ties to the lower index
+    assert orc.apportion([0, 0, 0], 4) == [2, 1, 1]        # all-zero weights -> uniform
+    assert orc.apportion([-1, 3], 5) == [0, 5]              # negatives clamp to 0
+    # Hamilton's method on a classic example: quotas 1.32, 3.37, 5.31 of 10 seats
+    assert orc.apportion([132, 337, 531], 10) == [1, 4, 5]
+    rnd = random.Random(0)
+    for _ in range(200):
+        n = rnd.randint(1, 9)
+        w = [rnd.random() for _ in range(n)]
+        total = rnd.randint(0, 50)
+        res = orc.apportion(w, total)
+        assert sum(res) == total
+        quota = [Fraction(total) * Fraction(x) / sum(map(Fraction, w)) for x in w]
+        assert all(abs(r - qv) < 1 for r, qv in zip(res, quota))  # quota rule
+    rows = orc.apportion_section_matrix([[1, 2], [3, 1]], 7)
+    assert rows == [orc.apportion([1, 2], 7), orc.apportion([3, 1], 7)]
+    assert all(sum(r) == 7 for r in rows)
+
+
+def test_budget_blocks_round_half_even():
+    assert orc.budget_blocks(0.25, 275) == 69    # 68.75
+    assert orc.budget_blocks(0.125, 275) == 34   # 34.375
+    assert orc.budget_blocks(0.5, 275) == 138    # 137.5 -> 138 (even)
+    assert orc.budget_blocks(0.5, 273) == 136    # 136.5 -> 136 (even)
+
+
+# ---------------------------------------------------------------- whole layer
+
+def test_rcsa_layer_composes_the_pinned_parts():
+    from cast_amd import workloads
+    w = workloads.plumbing(0)
+    res = orc.rcsa_layer(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=w.block_size,
+                         k_select=w.k_total, forced=w.forced)
+    qhat, _, _ = orc.pool_blocks(w.q, w.q_valid, w.block_size)
+    khat, _, _ = orc.pool_blocks(w.k, w.k_valid, w.block_size)
+    score = orc.block_scores(qhat, khat).reshape(res["score"].shape)
+    torch.testing.assert_close(res["score"], score)
+    # the current chunk's blocks are forced and so always selected
+    nh = w.n_hist_blocks
+    for r in range(res["indices"].shape[0]):
+        for i in range(res["indices"].shape[1]):
+            sel = set(res["indices"][r, i].tolist())
+            assert set(range(nh, w.n_kblocks)) <= sel
