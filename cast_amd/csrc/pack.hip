@@ -1,15 +1,38 @@
 // Compact-token <-> packed-block layout copies (HBM-bound gathers).
 //
-// One thread moves 8 channels (16 bytes of bf16 output) so that consecutive
-// threads write consecutive 16-byte chunks of a packed row.
+// One thread moves 8 channels so that consecutive threads write consecutive
+// chunks of a packed row.
 #include "rcsa_common.h"
 
 namespace rcsa {
 
 template <typename T>
+__device__ __forceinline__ void store8(T* dst, const float (&f)[8], bool live);
+
+template <>
+__device__ __forceinline__ void store8<u16>(u16* dst, const float (&f)[8], bool live) {
+  uint4 w = make_uint4(0, 0, 0, 0);
+  if (live) {
+    w.x = pack_bf16x2(f[0], f[1]);
+    w.y = pack_bf16x2(f[2], f[3]);
+    w.z = pack_bf16x2(f[4], f[5]);
+    w.w = pack_bf16x2(f[6], f[7]);
+  }
+  *reinterpret_cast<uint4*>(dst) = w;
+}
+
+template <>
+__device__ __forceinline__ void store8<float>(float* dst, const float (&f)[8], bool live) {
+  const float4 z = make_float4(0.f, 0.f, 0.f, 0.f);
+  reinterpret_cast<float4*>(dst)[0] = live ? make_float4(f[0], f[1], f[2], f[3]) : z;
+  reinterpret_cast<float4*>(dst)[1] = live ? make_float4(f[4], f[5], f[6], f[7]) : z;
+}
+
+// The packed copy keeps the source element type (a gather, no rounding).
+template <typename T>
 __global__ void __launch_bounds__(256)
 pack_kernel(const T* x, int64_t H, int64_t D, int64_t sb, int64_t sl, int64_t sh,
-            const int64_t* slot_token, int64_t n_slots, int64_t L, u16* out,
+            const int64_t* slot_token, int64_t n_slots, int64_t L, T* out,
             int64_t total_vec) {
   const int64_t v = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (v >= total_vec) return;
@@ -19,16 +42,10 @@ pack_kernel(const T* x, int64_t H, int64_t D, int64_t sb, int64_t sl, int64_t sh
   const int64_t bh = v / (cpr * n_slots);
   const int64_t b = bh / H, h = bh % H;
   const int64_t tok = slot_token[slot];
-  uint4 w = make_uint4(0, 0, 0, 0);
-  if (tok >= 0 && tok < L) {
-    float f[8];
-    Vec8<T>::load(x + b * sb + tok * sl + h * sh + c * 8, f);
-    w.x = pack_bf16x2(f[0], f[1]);
-    w.y = pack_bf16x2(f[2], f[3]);
-    w.z = pack_bf16x2(f[4], f[5]);
-    w.w = pack_bf16x2(f[6], f[7]);
-  }
-  *reinterpret_cast<uint4*>(out + (bh * n_slots + slot) * D + c * 8) = w;
+  const bool live = tok >= 0 && tok < L;
+  float f[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (live) Vec8<T>::load(x + b * sb + tok * sl + h * sh + c * 8, f);
+  store8<T>(out + (bh * n_slots + slot) * D + c * 8, f, live);
 }
 
 __global__ void __launch_bounds__(256)
@@ -71,7 +88,8 @@ extern "C" int rcsa_pack_tokens(const void* x, int dtype, int64_t B, int64_t L, 
   else
     pack_kernel<float><<<grid, dim3(256), 0, stream>>>(static_cast<const float*>(x), H, D,
                                                       stride_b, stride_l, stride_h, slot_token,
-                                                      n_slots, L, static_cast<u16*>(out), total);
+                                                      n_slots, L, static_cast<float*>(out),
+                                                      total);
   return launch_status();
 }
 

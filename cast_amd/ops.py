@@ -328,7 +328,7 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
 
 
 def pack_tokens(x: torch.Tensor, slot_token: torch.Tensor) -> torch.Tensor:
-    """Gather ``x [B, L, H, D]`` into packed ``[B, H, n_slots, D]`` bf16; slot -1 -> zeros.
+    """Gather ``x [B, L, H, D]`` into packed ``[B, H, n_slots, D]`` (x's dtype); slot -1 -> zeros.
 
     Mirrors ``q[:, flat].transpose(1, 2).contiguous(); q_packed[:, :, ~mask] = 0``
     (P/matrix_curvature_phase_frame_weave.py:5671-5684).
@@ -341,7 +341,7 @@ def pack_tokens(x: torch.Tensor, slot_token: torch.Tensor) -> torch.Tensor:
     B, L, H, D = x.shape
     st_ = slot_token.to(device=x.device, dtype=torch.int64).contiguous()
     n_slots = st_.numel()
-    out = torch.empty(B, H, n_slots, D, device=x.device, dtype=torch.bfloat16)
+    out = torch.empty(B, H, n_slots, D, device=x.device, dtype=x.dtype)
     check(_lib.load().rcsa_pack_tokens(x.data_ptr(), code, B, L, H, D, x.stride(0),
                                        x.stride(1), x.stride(2), st_.data_ptr(), n_slots,
                                        out.data_ptr(), _stream()), fn)

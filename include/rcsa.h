@@ -200,7 +200,7 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
  * at P/matrix_curvature_phase_frame_weave.py:5671-5684.
  *   x:      [B, L, H, D]   (strides in elements, last dim contiguous), bf16 or fp32
  *   slot_token: int64 [n_slots]  source token of each packed slot, -1 = invalid
- *   out:    [B, H, n_slots, D] bf16 (contiguous)
+ *   out:    [B, H, n_slots, D] (contiguous), same element type as x
  */
 int rcsa_pack_tokens(const void* x, int dtype, int64_t B, int64_t L, int64_t H,
                      int64_t D, int64_t stride_b, int64_t stride_l,

@@ -195,11 +195,16 @@ def test_pack_unpack_roundtrip(dev):
     slots = torch.full((6 * 128,), -1, dtype=torch.int64)
     perm = torch.randperm(L, generator=g)
     slots[: L] = perm
-    packed = ops.pack_tokens(x.to(dev), slots.to(dev))
     ref = torch.zeros(B, H, slots.numel(), D)
     ok = slots >= 0
     ref[:, :, ok] = x[:, slots[ok]].transpose(1, 2)
+    packed32 = ops.pack_tokens(x.to(dev), slots.to(dev))      # keeps fp32, no rounding
+    assert packed32.dtype == torch.float32 and torch.equal(packed32.cpu(), ref)
+    packed = ops.pack_tokens(x.to(dev, torch.bfloat16), slots.to(dev))
     assert torch.equal(packed.cpu(), ref.to(torch.bfloat16))
+    # a [B, H, L, D] tensor viewed as [B, L, H, D] packs without a copy
+    xt = x.transpose(1, 2).contiguous().to(dev)
+    assert torch.equal(ops.pack_tokens(xt.transpose(1, 2), slots.to(dev)).cpu(), ref)
     token_slot = torch.empty(L, dtype=torch.int64)
     token_slot[perm] = torch.arange(L)
     back = ops.unpack_tokens(packed, token_slot.to(dev))

@@ -234,3 +234,61 @@ def test_unaligned_valid_mask(dev):
         *v.stride()[:3], *out.stride()[:3], *idx.stride()[:3], *cnt.stride(), B, H, L, L, D,
         64, 128, 2, torch.cuda.current_stream().cuda_stream)
     assert st == 6  # RCSA_ERR_ALIGN, before any launch
+
+
+def _tile_visual(x, T, h, w, shape):
+    """[B, H, T*h*w, D] -> zero-padded (tt, th, tw) tiles [B, H, nb, bs, D]."""
+    tt, th, tw = shape
+    B, H, _, D = x.shape
+    x = x.reshape(B, H, T, h, w, D)
+    x = torch.nn.functional.pad(x, (0, 0, 0, (-w) % tw, 0, (-h) % th, 0, (-T) % tt))
+    nt, nh, nw = x.shape[2] // tt, x.shape[3] // th, x.shape[4] // tw
+    x = x.reshape(B, H, nt, tt, nh, th, nw, tw, D).permute(0, 1, 2, 4, 6, 3, 5, 7, 8)
+    return x.reshape(B, H, nt * nh * nw, tt * th * tw, D)
+
+
+@pytest.mark.parametrize("use_motion", [False, True])
+def test_selector_select_boundary(dev, use_motion):
+    """BlockSelector.select on the Matrix latent grid (22 x 40, 8 frames,
+    (4, 4, 8) tiles with 64-token bottom tiles) against the native rule:
+    normalise(tile mean) scores, +1e6 on the local stencil, stable
+    descending argsort, first max(row budget) columns."""
+    from cast_amd import layout, ops
+    from cast_amd.selector import BlockSelector
+    g = torch.Generator().manual_seed(11)
+    B, H, T, h, w, D, shape = 1, 2, 8, 22, 40, 64, (4, 4, 8)
+    frame_shift = torch.randn(B, H, T, 1, D, generator=g) * 0.3
+    q = (torch.randn(B, H, T, h * w, D, generator=g) + frame_shift).reshape(B, H, -1, D)
+    k = (torch.randn(B, H, T, h * w, D, generator=g) + frame_shift).reshape(B, H, -1, D)
+    nb = 2 * 6 * 5
+    sel = BlockSelector(shape, degree=16, num_blocks=nb)
+    motion = torch.rand(nb, generator=g) if use_motion else None
+    rows = sel.compile_budgets(token_h=h, token_w=w, ray_motion=motion)
+    geometry_counts = torch.full((B, H, nb), 16, dtype=torch.int32)
+    selected, counts, report = sel.select(q.to(dev), k.to(dev), geometry_indices=None,
+                                          geometry_counts=geometry_counts, latent_hw=(h, w),
+                                          block_shape=shape)
+    torch.cuda.synchronize()
+    max_deg = int(rows.max())
+    assert selected.shape == (B, H, nb, max_deg) and selected.dtype == torch.int32
+    assert torch.equal(counts.cpu(), rows.int()[None, None].expand(B, H, -1))
+    # the device's scores against fp32 tile means on the CPU
+    lay = layout.compact_layout(range(T), 0, h, w, shape, dev)
+    qhat, _, _ = ops.pool_query(ops.pack_tokens(q.to(dev).transpose(1, 2), lay.slot_token),
+                                lay.slot_valid, 128)
+    khat, _, _, _ = ops.pool_key(ops.pack_tokens(k.to(dev).transpose(1, 2), lay.slot_token),
+                                 lay.slot_valid, 128)
+    score_dev = ops.block_scores(qhat, khat).cpu().reshape(B, H, nb, nb)
+    qc = torch.nn.functional.normalize(_tile_visual(q, T, h, w, shape).mean(-2), dim=-1)
+    kc = torch.nn.functional.normalize(_tile_visual(k, T, h, w, shape).mean(-2), dim=-1)
+    score_cpu = qc @ kc.transpose(-1, -2)
+    assert float((score_dev - score_cpu).abs().max()) <= 1e-5
+    # bit-exact: the native rule applied to the device's scores
+    local = layout.local_stencil(nb, 6, 5)
+    ranking = score_dev + local[None, None].float() * 1e6
+    want = torch.argsort(ranking, dim=-1, descending=True, stable=True)[..., :max_deg]
+    assert torch.equal(selected.cpu().long(), want)
+    assert report.missing_local_edges == 0 and report.row_duplicate_violations == 0
+    assert report.protected_local_edges == int(local.sum()) * B * H
+    assert report.budget_total == int(rows.sum()) and report.budget_max == max_deg
+    assert report.query_rows == nb and report.batch_heads == B * H

@@ -1,0 +1,106 @@
+"""Host-side product logic against the pinned oracle (CPU only): the packed
+block layout, the local stencil, the budget arithmetic and the selector's
+argument checks."""
+import random
+
+import pytest
+import torch
+
+from cast_amd import budget, layout
+from cast_amd.selector import BlockSelector
+from oracle import rcsa_oracle as orc
+
+
+@pytest.mark.parametrize("frames,mem_t,H,W,shape", [
+    ([0, 1, 2, 3], 0, 8, 8, (2, 4, 4)),
+    ([0, 2, 5, 6, 7], 3, 6, 10, (2, 4, 4)),
+    ([1, 4], 2, 4, 4, (4, 2, 2)),
+    (list(range(8)), 4, 22, 40, (4, 4, 8)),   # Matrix latent grid: 64-token bottom tiles
+])
+def test_compact_layout_matches_oracle(frames, mem_t, H, W, shape):
+    lay = layout.compact_layout(frames, mem_t, H, W, shape)
+    idx, valid, t2p = orc.compact_layout(frames, mem_t, H, W, shape)
+    assert torch.equal(lay.block_indices, idx)
+    assert torch.equal(lay.block_valid, valid)
+    assert torch.equal(lay.token_to_packed, t2p)
+    assert lay.n_blocks == idx.shape[0] and lay.block_size == idx.shape[1]
+    assert torch.equal(lay.slot_token[lay.token_to_packed], torch.arange(t2p.numel()))
+
+
+def test_compact_layout_rejects_bad_input():
+    with pytest.raises(ValueError):
+        layout.compact_layout([], 0, 4, 4, (1, 2, 2))
+    with pytest.raises(ValueError):
+        layout.compact_layout([0], 0, 4, 4, (1, 2))
+
+
+@pytest.mark.parametrize("n,nh,nw", [(24, 2, 4), (60, 6, 5), (7, 1, 7)])
+def test_local_stencil_matches_oracle(n, nh, nw):
+    assert torch.equal(layout.local_stencil(n, nh, nw), orc.local_stencil(n, nh, nw))
+
+
+def test_apportion_matches_exact_arithmetic():
+    rnd = random.Random(1)
+    for _ in range(300):
+        n = rnd.randint(1, 40)
+        w = [rnd.random() * rnd.choice([1, 10, 1000]) for _ in range(n)]
+        total = rnd.randint(1, 400)
+        got = budget.apportion(torch.tensor(w), total).tolist()
+        # the oracle works in exact rationals on the fp32-rounded weights
+        w32 = torch.tensor(w, dtype=torch.float32).tolist()
+        want = orc.apportion(w32, total)
+        if got != want:
+            # only a sub-ulp tie between fractional parts may differ
+            raw = torch.tensor(w32) * total / sum(w32)
+            fr = sorted((raw - raw.floor()).tolist(), reverse=True)
+            assert any(abs(a - b) < 1e-5 for a, b in zip(fr, fr[1:]))
+        assert sum(got) == total
+
+
+def test_apportion_reference_errors_and_cases():
+    assert budget.apportion(torch.tensor([1.0, 1.0, 1.0]), 10).tolist() == [4, 3, 3]
+    assert budget.apportion(torch.tensor([0.0, 0.0]), 3).tolist() == [2, 1]
+    with pytest.raises(ValueError):
+        budget.apportion(torch.tensor([]), 3)
+    with pytest.raises(ValueError):
+        budget.apportion(torch.tensor([1.0]), 0)
+    m = torch.tensor([[1.0, 2.0, 3.0], [0.0, 0.0, 0.0], [5.0, 1.0, 1.0]])
+    got = budget.apportion_section_matrix(m, 8).tolist()
+    assert got == orc.apportion_section_matrix(m.tolist(), 8)
+    assert all(sum(r) == 8 for r in got)
+
+
+def test_budgets_and_saturation():
+    assert [budget.budget_blocks(f, 275) for f in (0.125, 0.25, 0.5)] == [34, 69, 138]
+    local = orc.local_stencil(24, 2, 4)
+    assert budget.mean_degree(local, 0.1, 24) == int(local.sum(1).max())
+    assert budget.mean_degree(local, 0.5, 24) == 12
+    d = budget.saturate(torch.tensor([30, 2, 2, 30]), 10, 40)
+    assert d.tolist() == [10, 10, 10, 10]
+    d = budget.saturate(torch.tensor([12, 1, 1]), 10, 14)
+    assert d.tolist() == [10, 2, 2] and int(d.sum()) == 14  # one each, lowest index first
+    motion = torch.rand(24, generator=torch.Generator().manual_seed(0))
+    rows = budget.motion_row_degrees(motion, 16, local)
+    assert int(rows.sum()) == 24 * 16 and int(rows.min()) >= int(local.sum(1).max())
+    w = 1.0 + motion / (motion.mean() + torch.finfo(torch.float32).eps)
+    assert rows.tolist() == budget.apportion(w, 24 * 16).tolist()
+    with pytest.raises(RuntimeError):
+        budget.motion_row_degrees(motion, 3, local)   # cannot hold the local stencil
+
+
+def test_selector_argument_checks():
+    sel = BlockSelector((4, 4, 8), degree=16, num_blocks=60)
+    q = torch.zeros(1, 2, 8 * 22 * 40, 64)
+    counts = torch.full((1, 2, 60), 16, dtype=torch.int32)
+    kw = dict(geometry_indices=None, geometry_counts=counts, latent_hw=(22, 40),
+              block_shape=(4, 4, 8))
+    with pytest.raises(RuntimeError, match="not compiled"):
+        sel.select(q, q, **kw)
+    rows = sel.compile_budgets(token_h=22, token_w=40)
+    assert rows.tolist() == [16] * 60
+    with pytest.raises(ValueError):
+        sel.select(q, q[:, :, :-1], **kw)
+    with pytest.raises(RuntimeError, match="block shape"):
+        sel.select(q, q, **{**kw, "block_shape": (2, 4, 8)})
+    with pytest.raises(RuntimeError, match="too small"):
+        sel.compile_budgets(token_h=22, token_w=40, row_degrees=torch.full((60,), 3))
