@@ -165,7 +165,8 @@ sparse_attn_kernel(AttnArgs a) {
   const int64_t b = bh / a.H, h = bh % a.H;
 
   const int tid = threadIdx.x;
-  const int lane = tid % kWave, wave = tid / kWave;
+  const int lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // uniform: SGPR arithmetic
   const int rg = wave % C::NRG, kh = wave / C::NRG;
   const int hf = lane >> 5, lr = lane & 31;
   const int64_t qrow = qb * BM + rg * 32 + lr;
@@ -296,30 +297,42 @@ sparse_attn_kernel(AttnArgs a) {
     }
   }
 
+  // The first MFMA of every S tile accumulates onto this constant tile (the
+  // 1.5 * 2^23 pattern for int8, zero for bf16): no per-block moves.
+  AccT c_init;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    if constexpr (INT8) c_init[r] = kMagicI;
+    else c_init[r] = 0.0f;
+  }
+
   // One key block from the slot at `tile`.
   auto compute = [&](const char* tile, int64_t n, float kscale) __attribute__((always_inline)) {
     const uint64_t vmask = __ballot(key_valid(n, tile));
     const bool all_valid = vmask == (~0ull >> (64 - C::HK));
-    // ---- S^T = K Q^T ----
+    // ---- S^T = K Q^T: every K operand read is issued before the MFMAs ----
     AccT s_acc[C::KT];
+    v4i kraw[C::KT][C::QSTEPS];
 #pragma unroll
-    for (int t = 0; t < C::KT; ++t) {
+    for (int t = 0; t < C::KT; ++t)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if constexpr (INT8) s_acc[t][r] = kMagicI;
-        else s_acc[t][r] = 0.0f;
-      }
+      for (int st = 0; st < C::QSTEPS; ++st)
+        kraw[t][st] = *reinterpret_cast<const v4i*>(tile + k_off[st] + 32 * t * C::KROW);
 #pragma unroll
-      for (int st = 0; st < C::QSTEPS; ++st) {
-        const v4i raw = *reinterpret_cast<const v4i*>(tile + k_off[st] + 32 * t * C::KROW);
+    for (int st = 0; st < C::QSTEPS; ++st)
+#pragma unroll
+      for (int t = 0; t < C::KT; ++t) {
         if constexpr (INT8) {
-          s_acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(raw, q_op[st], s_acc[t], 0, 0, 0);
+          s_acc[t] = __builtin_amdgcn_mfma_i32_32x32x32_i8(kraw[t][st], q_op[st],
+                                                           st == 0 ? c_init : s_acc[t], 0, 0, 0);
         } else {
           s_acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-              __builtin_bit_cast(v8bf, raw), q_op[st], s_acc[t], 0, 0, 0);
+              __builtin_bit_cast(v8bf, kraw[t][st]), q_op[st], st == 0 ? c_init : s_acc[t],
+              0, 0, 0);
         }
       }
-    }
+    __builtin_amdgcn_sched_group_barrier(0x100, C::KT * C::QSTEPS, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, C::KT * C::QSTEPS, 0);
     // ---- online softmax: lane half hf, register r <-> key 32t + 16hf + r ----
     // raw value: int8 -> 1.5*2^23 + x read as fp32; bf16 -> the fp32 logit.
     // A masked key's raw value becomes -inf, so max and exp2 need no mask.
@@ -379,21 +392,37 @@ sparse_attn_kernel(AttnArgs a) {
           l_run = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_run, false);
         }
       }
-    // ---- O^T += V^T P^T, V^T operand by transposing LDS reads ----
+    // ---- O^T += V^T P^T, V^T operand by transposing LDS reads; the reads of
+    //      the next 16-key step are in flight during this step's MFMAs ----
+    auto v_group = [&](int g, v8bf (&op)[C::NDT]) __attribute__((always_inline)) {
+      const int t = g >> 1, u = g & 1;
 #pragma unroll
-    for (int t = 0; t < C::KT; ++t)
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        const char* p0 = tile + v_off[dt] + (32 * t + 8 * u) * C::VROW;
+        const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0));
+        const v4bf hi =
+            __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0 + 4 * C::VROW));
+        op[dt] = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+      }
+    };
+    v8bf vop[2][C::NDT];
+    v_group(0, vop[0]);
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+    for (int g = 0; g < 2 * C::KT; ++g) {
+      if (g + 1 < 2 * C::KT) v_group(g + 1, vop[(g + 1) & 1]);
 #pragma unroll
-        for (int dt = 0; dt < C::NDT; ++dt) {
-          const char* p0 = tile + v_off[dt] + (32 * t + 8 * u) * C::VROW;
-          const v4bf lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0));
-          const v4bf hi =
-              __builtin_amdgcn_ds_read_tr16_b64_v4bf16(RCSA_LDS(v4bf, p0 + 4 * C::VROW));
-          const v8bf v_op = __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
-          o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(v_op, p_op[t][u], o_acc[dt],
-                                                             0, 0, 0);
-        }
+      for (int dt = 0; dt < C::NDT; ++dt)
+        o_acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[g & 1][dt], p_op[g >> 1][g & 1],
+                                                           o_acc[dt], 0, 0, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x100, 2 * C::NDT, 0);
+#pragma unroll
+    for (int g = 0; g < 2 * C::KT; ++g)
+#pragma unroll
+      for (int dt = 0; dt < C::NDT; ++dt) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (g + 1 < 2 * C::KT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
   };
 
   // ---- ring: block j lives in slot j % STAGES; STAGES-1 blocks in flight ----

@@ -187,6 +187,36 @@ def test_sparse_attn_int8(dev, D, bs):
     _check_out(out, ref32, qv, "int8 vs fp32 oracle")
 
 
+@pytest.mark.parametrize("lk", [9 * 128 + 37, 128, 100])
+def test_sparse_attn_int8_ragged_keys(dev, lk):
+    """int8 attention over a key length that is not a whole number of blocks
+    (the last block is partial), exactly one block, and less than one block."""
+    from cast_amd import ops
+    g = torch.Generator().manual_seed(lk)
+    B, H, D, bs, lq = 1, 2, 128, 128, 2 * 128
+    nkb = -(-lk // bs)
+    q8 = torch.randint(-127, 128, (B, H, lq, D), generator=g, dtype=torch.int8)
+    k8 = torch.randint(-127, 128, (B, H, lk, D), generator=g, dtype=torch.int8)
+    v = torch.randn(B, H, lk, D, generator=g).to(torch.bfloat16)
+    qs = torch.rand(B * H, lq // bs, generator=g) * 0.02 + 0.005
+    ks = torch.rand(B * H, nkb, generator=g) * 0.02 + 0.005
+    kv = torch.rand(lk, generator=g) < 0.9
+    idx, cnt = _lists((B, H), lq // bs, nkb, nkb, 13)
+    idx[..., 0] = nkb - 1  # every row reads the partial last block
+    cnt.clamp_(min=1)
+    out, lse = ops.sparse_attn_int8(q8.to(dev), qs.to(dev), k8.to(dev), ks.to(dev), v.to(dev),
+                                    idx.to(dev), cnt.to(dev), kv.to(dev), return_lse=True)
+    qf = (q8.float().reshape(B, H, lq // bs, bs, D) * qs.reshape(B, H, -1, 1, 1)).reshape(q8.shape)
+    kblk = torch.arange(lk) // bs
+    kf = k8.float() * ks.reshape(B, H, nkb)[:, :, kblk, None]
+    ref, rlse = orc.sparse_attention(qf, kf, v.float(), idx, cnt, kv, block_m=bs, block_n=bs)
+    _check_out(out, ref, torch.ones(lq, dtype=torch.bool), f"int8 ragged lk={lk}",
+               cos_min=0.9999, rel=5e-3)
+    fin = torch.isfinite(rlse)
+    assert torch.equal(fin, torch.isfinite(lse.cpu()))
+    torch.testing.assert_close(lse.cpu()[fin], rlse[fin], atol=2e-2, rtol=0)
+
+
 def test_pack_unpack_roundtrip(dev):
     from cast_amd import ops
     g = torch.Generator().manual_seed(7)
