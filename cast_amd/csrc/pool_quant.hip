@@ -43,19 +43,74 @@ __device__ __forceinline__ float block_max(float v, float* red) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// Sum / min / max of v over the row groups that share a wavefront: lanes
+// with the same channel chunk (lane % CPR) are combined by xor shuffles.
+template <int CPR>
+__device__ __forceinline__ float wave_rows_sum(float v) {
+#pragma unroll
+  for (int o = CPR; o < kWave; o <<= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+template <int CPR>
+__device__ __forceinline__ float wave_rows_min(float v) {
+#pragma unroll
+  for (int o = CPR; o < kWave; o <<= 1) v = fminf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+template <int CPR>
+__device__ __forceinline__ float wave_rows_max(float v) {
+#pragma unroll
+  for (int o = CPR; o < kWave; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+// Raw 16-byte chunks of a tile row (8 elements): bf16 keeps one uint4, fp32 two.
+template <typename T>
+struct Raw8;
+template <>
+struct Raw8<u16> {
+  uint4 w;
+  __device__ __forceinline__ void load(const u16* p) { w = *reinterpret_cast<const uint4*>(p); }
+  __device__ __forceinline__ void get(float* out) const {
+    const uint32_t v[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(v[i] << 16);
+      out[2 * i + 1] = __uint_as_float(v[i] & 0xffff0000u);
+    }
+  }
+};
+template <>
+struct Raw8<float> {
+  float4 a, b;
+  __device__ __forceinline__ void load(const float* p) {
+    a = reinterpret_cast<const float4*>(p)[0];
+    b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void get(float* out) const {
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  }
+};
+
 // One workgroup per (bh, block).  QUANT: fuse the int8 query quantiser.
-// STATS: write sum/min/max for the key quantiser.
+// STATS: write sum/min/max for the key quantiser.  Every thread issues all
+// its row loads first; the block's validity bytes go through LDS while they
+// are in flight, and the per-channel partials are reduced across the row
+// groups of a wavefront by shuffles before one small LDS pass.
 template <typename T, int D, int BS, bool QUANT, bool STATS>
 __global__ void __launch_bounds__(kPoolThreads)
 pool_kernel(PoolArgs a) {
   constexpr int CPR = D / 8;                 // 16-byte chunks per token row
   constexpr int RG = kPoolThreads / CPR;     // row groups
   constexpr int ROWS = BS / RG;              // rows per thread
-  static_assert(ROWS >= 1 && RG * CPR == kPoolThreads, "tile shape");
+  constexpr int NWV = kPoolThreads / kWave;  // wavefronts
+  static_assert(ROWS >= 1 && RG * CPR == kPoolThreads && CPR <= kWave, "tile shape");
 
-  __shared__ float s_sum[RG][D];
-  __shared__ float s_min[STATS ? RG : 1][D];
-  __shared__ float s_max[STATS ? RG : 1][D];
+  __shared__ float s_sum[NWV][D];
+  __shared__ float s_min[STATS ? NWV : 1][D];
+  __shared__ float s_max[STATS ? NWV : 1][D];
+  __shared__ uint8_t s_valid[BS];
   __shared__ float s_red[4];
 
   const int64_t blk = blockIdx.x % a.n_blocks;
@@ -65,23 +120,27 @@ pool_kernel(PoolArgs a) {
                blk * BS * a.stride_t;
   const int t = threadIdx.x;
   const int c = t % CPR, g = t / CPR;
+  const int lane = t % kWave, wave = t / kWave;
 
-  const int n_valid = __syncthreads_count(
-      t < BS && (a.valid == nullptr || a.valid[blk * BS + t] != 0));
+  Raw8<T> raw[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i) raw[i].load(x + (g + RG * i) * a.stride_t + c * 8);
+  bool tv = false;
+  if (t < BS) {
+    tv = a.valid == nullptr || a.valid[blk * BS + t] != 0;
+    s_valid[t] = tv;
+  }
+  const int n_valid = __syncthreads_count(tv);
 
-  float vals[QUANT ? ROWS : 1][8];
-  bool rv[ROWS];
   float sum[8], mn[8], mx[8];
   float amax = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) { sum[j] = 0.0f; mn[j] = INFINITY; mx[j] = -INFINITY; }
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
-    const int r = g + RG * i;
-    rv[i] = a.valid == nullptr || a.valid[blk * BS + r] != 0;
-    float v[8];
-    Vec8<T>::load(x + r * a.stride_t + c * 8, v);
-    if (rv[i]) {
+    if (s_valid[g + RG * i]) {
+      float v[8];
+      raw[i].get(v);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         sum[j] += v[j];
@@ -89,25 +148,30 @@ pool_kernel(PoolArgs a) {
         if (QUANT) amax = fmaxf(amax, fabsf(v[j]));
       }
     }
-    if (QUANT) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) vals[i][j] = v[j];
-    }
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
-    s_sum[g][c * 8 + j] = sum[j];
-    if (STATS) { s_min[g][c * 8 + j] = mn[j]; s_max[g][c * 8 + j] = mx[j]; }
+    sum[j] = wave_rows_sum<CPR>(sum[j]);
+    if (STATS) { mn[j] = wave_rows_min<CPR>(mn[j]); mx[j] = wave_rows_max<CPR>(mx[j]); }
   }
+  if (lane < CPR) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      s_sum[wave][c * 8 + j] = sum[j];
+      if (STATS) { s_min[wave][c * 8 + j] = mn[j]; s_max[wave][c * 8 + j] = mx[j]; }
+    }
+  }
+  if (QUANT) amax = wave_max(amax);
+  if (QUANT && lane == 0) s_red[wave] = amax;
   __syncthreads();
 
   float mean = 0.0f;
   if (t < D) {
     float s = 0.0f, lo = INFINITY, hi = -INFINITY;
-#pragma unroll 4
-    for (int r = 0; r < RG; ++r) {
-      s += s_sum[r][t];
-      if (STATS) { lo = fminf(lo, s_min[r][t]); hi = fmaxf(hi, s_max[r][t]); }
+#pragma unroll
+    for (int w = 0; w < NWV; ++w) {
+      s += s_sum[w][t];
+      if (STATS) { lo = fminf(lo, s_min[w][t]); hi = fmaxf(hi, s_max[w][t]); }
     }
     const int64_t o = (bh * a.n_blocks + blk) * D + t;
     if (STATS) {
@@ -118,6 +182,7 @@ pool_kernel(PoolArgs a) {
     }
     mean = s / static_cast<float>(n_valid > 0 ? n_valid : 1);
   }
+  if (QUANT) amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
   const float norm2 = block_sum(t < D ? mean * mean : 0.0f, s_red);
   if (t < D) {
     const float denom = fmaxf(sqrtf(norm2), 1e-12f);
@@ -125,7 +190,6 @@ pool_kernel(PoolArgs a) {
   }
 
   if (QUANT) {
-    amax = block_max(amax, s_red);
     const float scale = amax > 0.0f ? amax / 127.0f : 1.0f;
     const float inv = amax > 0.0f ? 127.0f / amax : 1.0f;
     if (t == 0) a.x_scale[bh * a.n_blocks + blk] = scale;
@@ -134,11 +198,13 @@ pool_kernel(PoolArgs a) {
     for (int i = 0; i < ROWS; ++i) {
       const int r = g + RG * i;
       uint32_t lo = 0, hi = 0;
-      if (rv[i]) {
+      if (s_valid[r]) {
+        float v[8];
+        raw[i].get(v);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          lo |= (static_cast<uint32_t>(quant_i8(vals[i][j], inv)) & 0xffu) << (8 * j);
-          hi |= (static_cast<uint32_t>(quant_i8(vals[i][j + 4], inv)) & 0xffu) << (8 * j);
+          lo |= (static_cast<uint32_t>(quant_i8(v[j], inv)) & 0xffu) << (8 * j);
+          hi |= (static_cast<uint32_t>(quant_i8(v[j + 4], inv)) & 0xffu) << (8 * j);
         }
       }
       *reinterpret_cast<uint2*>(out + r * D + c * 8) = make_uint2(lo, hi);
@@ -147,26 +213,48 @@ pool_kernel(PoolArgs a) {
 }
 
 // Cosine scores: one workgroup per (bh, 16 query blocks, 64 key blocks).
+// The tiles are loaded with 16-byte loads, all issued before the LDS stores.
 template <int D>
 __global__ void __launch_bounds__(256)
 score_kernel(const float* qhat, const float* khat, int64_t nq, int64_t nk,
              float* score) {
   __shared__ float sq[16][D];
   __shared__ float sk[64][D + 1];
+  constexpr int C4 = D / 4;                      // float4 per row
+  constexpr int QL = 16 * C4 / 256;              // float4 loads per thread (query tile)
+  constexpr int KL = 64 * C4 / 256;              // (key tile)
   const int64_t tiles_q = (nq + 15) / 16, tiles_k = (nk + 63) / 64;
   const int64_t tk = blockIdx.x % tiles_k;
   const int64_t tq = (blockIdx.x / tiles_k) % tiles_q;
   const int64_t bh = blockIdx.x / (tiles_k * tiles_q);
   const int t = threadIdx.x;
-  const float* qb = qhat + (bh * nq + tq * 16) * D;
-  const float* kb = khat + (bh * nk + tk * 64) * D;
-  for (int e = t; e < 16 * D; e += 256) {
-    const int r = e / D, cc = e % D;
-    sq[r][cc] = (tq * 16 + r < nq) ? qb[r * D + cc] : 0.0f;
+  const float4* qb = reinterpret_cast<const float4*>(qhat + (bh * nq + tq * 16) * D);
+  const float4* kb = reinterpret_cast<const float4*>(khat + (bh * nk + tk * 64) * D);
+  // rows past the end re-read the last row (then zeroed): every load is in bounds
+  float4 qv[QL], kv[KL];
+  const int q_last = static_cast<int>(min<int64_t>(nq - tq * 16, 16)) - 1;
+  const int k_last = static_cast<int>(min<int64_t>(nk - tk * 64, 64)) - 1;
+#pragma unroll
+  for (int i = 0; i < QL; ++i) {
+    const int e = t + 256 * i, r = e / C4;
+    qv[i] = qb[min(r, q_last) * C4 + e % C4];
+    if (r > q_last) qv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
-  for (int e = t; e < 64 * D; e += 256) {
-    const int r = e / D, cc = e % D;
-    sk[r][cc] = (tk * 64 + r < nk) ? kb[r * D + cc] : 0.0f;
+#pragma unroll
+  for (int i = 0; i < KL; ++i) {
+    const int e = t + 256 * i, r = e / C4;
+    kv[i] = kb[min(r, k_last) * C4 + e % C4];
+    if (r > k_last) kv[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+  }
+#pragma unroll
+  for (int i = 0; i < QL; ++i) {
+    const int e = t + 256 * i, r = e / C4, cc = (e % C4) * 4;
+    sq[r][cc] = qv[i].x; sq[r][cc + 1] = qv[i].y; sq[r][cc + 2] = qv[i].z; sq[r][cc + 3] = qv[i].w;
+  }
+#pragma unroll
+  for (int i = 0; i < KL; ++i) {
+    const int e = t + 256 * i, r = e / C4, cc = (e % C4) * 4;
+    sk[r][cc] = kv[i].x; sk[r][cc + 1] = kv[i].y; sk[r][cc + 2] = kv[i].z; sk[r][cc + 3] = kv[i].w;
   }
   __syncthreads();
   const int qi = t / 16;
@@ -181,54 +269,61 @@ score_kernel(const float* qhat, const float* khat, int64_t nq, int64_t nk,
   }
 }
 
+// Number of nonzero bytes of a 32-bit word.
+__device__ __forceinline__ int nonzero_bytes(uint32_t w) {
+  return __popc((((w & 0x7f7f7f7fu) + 0x7f7f7f7fu) | w) & 0x80808080u);
+}
+
 // Per-head key mean over all valid tokens: kmean = sum_b ksum / n_valid_total.
-// One workgroup per head; the block loop is unrolled with independent
-// partial sums so that many loads are in flight (the pass is latency bound).
+// One workgroup per (bh, 16 channels): 16 block lanes per channel, each with
+// four independent partial sums, then an LDS reduction.  The valid-token
+// count is taken with 16-byte loads.
 template <int D>
 __global__ void __launch_bounds__(256)
 kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
              int64_t n_tokens, float* kmean) {
-  constexpr int G = 256 / D;
-  constexpr int U = 8;
-  __shared__ float part[G][D];
+  constexpr int CG = 16;          // channels per workgroup
+  constexpr int BL = 256 / CG;    // block lanes
+  __shared__ float part[BL][CG + 1];
   __shared__ float s_red[4];
-  const int64_t bh = blockIdx.x;
-  const int t = threadIdx.x, c = t % D, g = t / D;
-  const float* src = ksum + bh * n_blocks * D + c;
-  float acc[U];
+  const int64_t bh = blockIdx.x / (D / CG);
+  const int c0 = static_cast<int>(blockIdx.x % (D / CG)) * CG;
+  const int t = threadIdx.x, c = t % CG, bl = t / CG;
+  const float* src = ksum + bh * n_blocks * D + c0 + c;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int64_t b = bl;
+  for (; b + 3 * BL < n_blocks; b += 4 * BL) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) acc[u] = 0.0f;
-  int64_t b = g;
-  for (; b + (U - 1) * G < n_blocks; b += U * G) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) acc[u] += src[(b + u * G) * D];
+    for (int u = 0; u < 4; ++u) acc[u] += src[(b + u * BL) * D];
   }
-  for (; b < n_blocks; b += G) acc[0] += src[b * D];
-  float s = 0.0f;
-#pragma unroll
-  for (int u = 0; u < U; ++u) s += acc[u];
-  part[g][c] = s;
+  for (; b < n_blocks; b += BL) acc[0] += src[b * D];
+  part[bl][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   int cnt = 0;
   if (valid == nullptr) {
     cnt = t == 0 ? static_cast<int>(n_tokens) : 0;
-  } else {
-    int64_t i = t;
-    for (; i + 7 * 256 < n_tokens; i += 8 * 256) {
-#pragma unroll
-      for (int u = 0; u < 8; ++u) cnt += valid[i + u * 256] != 0;
+  } else if ((reinterpret_cast<uintptr_t>(valid) & 15u) == 0) {
+    const int64_t n16 = n_tokens / 16;
+    const uint4* v4 = reinterpret_cast<const uint4*>(valid);
+    for (int64_t i = t; i < n16; i += 256) {
+      const uint4 w = v4[i];
+      cnt += nonzero_bytes(w.x) + nonzero_bytes(w.y) + nonzero_bytes(w.z) + nonzero_bytes(w.w);
     }
-    for (; i < n_tokens; i += 256) cnt += valid[i] != 0;
+    for (int64_t i = n16 * 16 + t; i < n_tokens; i += 256) cnt += valid[i] != 0;
+  } else {
+    for (int64_t i = t; i < n_tokens; i += 256) cnt += valid[i] != 0;
   }
-  const float total = block_sum(static_cast<float>(cnt), s_red);
-  if (t < D) {
+  const float total = block_sum(static_cast<float>(cnt), s_red);  // also publishes part
+  if (t < CG) {
     float sum = 0.0f;
 #pragma unroll
-    for (int i = 0; i < G; ++i) sum += part[i][t];
-    kmean[bh * D + t] = sum / fmaxf(total, 1.0f);
+    for (int i = 0; i < BL; ++i) sum += part[i][t];
+    kmean[bh * D + c0 + t] = sum / fmaxf(total, 1.0f);
   }
 }
 
-// Smoothed per-block key quantiser: one workgroup per (bh, block).
+// Smoothed per-block key quantiser: one workgroup per (bh, block).  The tile
+// loads are issued first; the scale (from the block's min/max and the head
+// mean) is computed while they are in flight.
 template <typename T, int D, int BS>
 __global__ void __launch_bounds__(kPoolThreads)
 quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
@@ -236,13 +331,23 @@ quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
   constexpr int RG = kPoolThreads / CPR;
   constexpr int ROWS = BS / RG;
   __shared__ float s_mean[D];
+  __shared__ uint8_t s_valid[BS];
   __shared__ float s_red[4];
   const int64_t blk = blockIdx.x % a.n_blocks;
   const int64_t bh = blockIdx.x / a.n_blocks;
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
   const int t = threadIdx.x;
-  const int n_valid = __syncthreads_count(
-      t < BS && (a.valid == nullptr || a.valid[blk * BS + t] != 0));
+  const int c = t % CPR, g = t / CPR;
+  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
+               blk * BS * a.stride_t;
+  Raw8<T> raw[ROWS];
+#pragma unroll
+  for (int i = 0; i < ROWS; ++i) raw[i].load(x + (g + RG * i) * a.stride_t + c * 8);
+  bool tv = false;
+  if (t < BS) {
+    tv = a.valid == nullptr || a.valid[blk * BS + t] != 0;
+    s_valid[t] = tv;
+  }
   float dev = 0.0f;
   if (t < D) {
     const float m = kmean[bh * D + t];
@@ -250,27 +355,24 @@ quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
     const int64_t o = (bh * a.n_blocks + blk) * D + t;
     dev = fmaxf(a.bmax[o] - m, m - a.bmin[o]);
   }
-  const float amax = block_max(dev, s_red);  // also publishes s_mean
+  const int n_valid = __syncthreads_count(tv);
+  const float amax = block_max(dev, s_red);  // also publishes s_mean / s_valid
   const bool live = n_valid > 0 && amax > 0.0f;
   const float scale = live ? amax / 127.0f : 1.0f;
   const float inv = live ? 127.0f / amax : 1.0f;
   if (t == 0) k_scale[bh * a.n_blocks + blk] = scale;
 
-  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
-               blk * BS * a.stride_t;
   int8_t* out = k_i8 + (bh * a.n_blocks + blk) * BS * D;
-  const int c = t % CPR, g = t / CPR;
   float m8[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) m8[j] = s_mean[c * 8 + j];
 #pragma unroll
   for (int i = 0; i < ROWS; ++i) {
     const int r = g + RG * i;
-    const bool ok = a.valid == nullptr || a.valid[blk * BS + r] != 0;
-    float v[8];
-    Vec8<T>::load(x + r * a.stride_t + c * 8, v);
     uint32_t lo = 0, hi = 0;
-    if (ok) {
+    if (s_valid[r]) {
+      float v[8];
+      raw[i].get(v);
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         lo |= (static_cast<uint32_t>(quant_i8(v[j] - m8[j], inv)) & 0xffu) << (8 * j);
@@ -387,8 +489,10 @@ extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
   if (!aligned16(k) || (reinterpret_cast<uintptr_t>(k_i8) & 7u)) return RCSA_ERR_ALIGN;
   const int64_t nbh = batch * n_heads;
   const int64_t n_tokens = n_blocks * block_size;
-  if (head_dim == 128) kmean_kernel<128><<<dim3(nbh), dim3(256), 0, stream>>>(ksum, valid, n_blocks, n_tokens, kmean);
-  else kmean_kernel<64><<<dim3(nbh), dim3(256), 0, stream>>>(ksum, valid, n_blocks, n_tokens, kmean);
+  if (head_dim == 128)
+    kmean_kernel<128><<<dim3(nbh * 8), dim3(256), 0, stream>>>(ksum, valid, n_blocks, n_tokens, kmean);
+  else
+    kmean_kernel<64><<<dim3(nbh * 4), dim3(256), 0, stream>>>(ksum, valid, n_blocks, n_tokens, kmean);
   st = launch_status();
   if (st) return st;
   PoolArgs a{k, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, nullptr,
