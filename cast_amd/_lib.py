@@ -32,6 +32,12 @@ SIGNATURES: dict[str, list] = {
                              + [_I] * 8 + [_P],
     "rcsa_sparse_attn_int8": [_P, _P, _I, _P, _P, _I, _P, _P, c_float, _P, _P, _P, _P]
                              + [_I] * 18 + [_I] * 8 + [_P],
+    "rcsa_sparse_attn_bf16_split": [_P, _P, _P, _P, c_float, _P, _P, _P, _P] + [_I] * 18
+                                   + [_I] * 8 + [_I, _P, _I, _P],
+    "rcsa_sparse_attn_int8_split": [_P, _P, _I, _P, _P, _I, _P, _P, c_float, _P, _P, _P, _P]
+                                   + [_I] * 18 + [_I] * 8 + [_I, _P, _I, _P],
+    "rcsa_attn_workspace_bytes": [_I, _I, _I, _I, _I],
+    "rcsa_attn_split_plan": [_I, _I, _I, _I, _I, ctypes.POINTER(c_int64)],
     "rcsa_pack_tokens": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "rcsa_unpack_tokens": [_P, _I, _I, _I, _I, _P, _I, _P, _P],
     "rcsa_status_string": [c_int],
@@ -55,7 +61,8 @@ def load() -> ctypes.CDLL:
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
         fn.argtypes = argtypes
-        fn.restype = ctypes.c_char_p if name == "rcsa_status_string" else c_int
+        fn.restype = (ctypes.c_char_p if name == "rcsa_status_string"
+                      else c_int64 if name == "rcsa_attn_workspace_bytes" else c_int)
     _lib = lib
     return lib
 

@@ -57,6 +57,12 @@ struct AttnArgs {
   int64_t sqz, sqh, sqm, skz, skh, skn, svz, svh, svn, soz, soh, som;
   int64_t sbz, sbh, sbm, slz, slh, slm;
   int64_t H, q_len, k_len, n_qblocks, n_kblocks, max_k, n_work;
+  // split of every block list over n_split workgroups (1 = no split); the
+  // partial results go to ws_o [n_split][B*H][q_len][D] bf16 (normalised) and
+  // ws_ml [n_split][B*H][q_len] (m, l) for attn_merge_kernel
+  int64_t n_split, n_bh;
+  u16* ws_o;
+  float2* ws_ml;
 };
 
 constexpr float kTau = 8.0f;               // lazy-rescale threshold, log2 units
@@ -160,8 +166,11 @@ sparse_attn_kernel(AttnArgs a) {
 
   const int64_t work = xcd_remap(blockIdx.x, a.n_work);
   if (work < 0) return;
-  const int64_t qb = work % a.n_qblocks;
-  const int64_t bh = work / a.n_qblocks;
+  // consecutive work items: the splits of one query block, then the next
+  // query block of the same head (neighbours share an XCD's L2)
+  const int64_t split = work % a.n_split;
+  const int64_t qb = (work / a.n_split) % a.n_qblocks;
+  const int64_t bh = work / (a.n_split * a.n_qblocks);
   const int64_t b = bh / a.H, h = bh % a.H;
 
   const int tid = threadIdx.x;
@@ -201,6 +210,11 @@ sparse_attn_kernel(AttnArgs a) {
   int64_t cnt = a.lens[b * a.slz + h * a.slh + qb * a.slm];
   cnt = cnt < 0 ? 0 : (cnt > a.max_k ? a.max_k : cnt);
   const int32_t* list = a.idx + b * a.sbz + h * a.sbh + qb * a.sbm;
+  {  // this workgroup's share of the list (shares differ by at most one block)
+    const int64_t begin = cnt * split / a.n_split, end = cnt * (split + 1) / a.n_split;
+    list += begin;
+    cnt = end - begin;
+  }
   const char* kbase = static_cast<const char*>(a.k) + (b * a.skz + h * a.skh) * C::KB;
   const char* vbase = reinterpret_cast<const char*>(a.v + b * a.svz + h * a.svh);
   const int64_t klast = a.k_len - 1;
@@ -504,7 +518,10 @@ sparse_attn_kernel(AttnArgs a) {
     const float inv = l > 0.0f ? 1.0f / l : 0.0f;
     const float fa = wa * inv, fb = wb * inv;
     if (qrow_ok) {
-      u16* op = a.out + b * a.soz + h * a.soh + qrow * a.som;
+      // a split writes its normalised partial and (m, l) to the workspace
+      const int64_t ws_row = (split * a.n_bh + bh) * a.q_len + qrow;
+      u16* op = a.n_split == 1 ? a.out + b * a.soz + h * a.soh + qrow * a.som
+                               : a.ws_o + ws_row * D;
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
@@ -519,11 +536,56 @@ sparse_attn_kernel(AttnArgs a) {
           *reinterpret_cast<uint2*>(op + d0) =
               make_uint2(pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3]));
         }
-      if (a.lse && hf == 0)
-        a.lse[(b * a.H + h) * a.q_len + qrow] =
-            l > 0.0f ? (m + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+      if (hf == 0) {
+        if (a.n_split > 1) {
+          a.ws_ml[ws_row] = make_float2(l > 0.0f ? m : -INFINITY, l);
+        } else if (a.lse) {
+          a.lse[(b * a.H + h) * a.q_len + qrow] =
+              l > 0.0f ? (m + __log2f(l)) * 0.69314718055994531f : -INFINITY;
+        }
+      }
     }
   }
+}
+
+// Combine the n_split partial results of every query row:
+//   w_s = l_s 2^(m_s - M),  out = sum_s w_s O_s / sum_s w_s,  lse = ln 2 (M + log2 sum_s w_s)
+// One thread per (row, 8 channels); rows with no admissible key get 0 / -inf.
+template <int D>
+__global__ void __launch_bounds__(256)
+attn_merge_kernel(AttnArgs a) {
+  const int64_t n_bh = a.n_bh;
+  constexpr int CPR = D / 8;
+  const int64_t v = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  const int64_t rows = n_bh * a.q_len;
+  if (v >= rows * CPR) return;
+  const int c = static_cast<int>(v % CPR);
+  const int64_t row = v / CPR;  // bh * q_len + qrow
+  const int64_t bh = row / a.q_len, qrow = row % a.q_len;
+  float mx = -INFINITY;
+  for (int64_t s = 0; s < a.n_split; ++s) mx = fmaxf(mx, a.ws_ml[s * rows + row].x);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float wsum = 0.0f;
+  if (mx != -INFINITY) {
+    for (int64_t s = 0; s < a.n_split; ++s) {
+      const float2 ml = a.ws_ml[s * rows + row];
+      if (ml.x == -INFINITY) continue;
+      const float w = ml.y * __builtin_amdgcn_exp2f(ml.x - mx);
+      wsum += w;
+      float o[8];
+      Vec8<u16>::load(a.ws_o + (s * rows + row) * D + c * 8, o);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j] = fmaf(w, o[j], acc[j]);
+    }
+  }
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  const int64_t b = bh / a.H, h = bh % a.H;
+  u16* op = a.out + b * a.soz + h * a.soh + qrow * a.som + c * 8;
+  *reinterpret_cast<uint4*>(op) =
+      make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
+                 pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv));
+  if (a.lse && c == 0)
+    a.lse[row] = wsum > 0.0f ? (mx + __log2f(wsum)) * 0.69314718055994531f : -INFINITY;
 }
 
 template <bool INT8>
@@ -546,6 +608,41 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
   RCSA_ATTN(64, 64, 64, 2)
 #undef RCSA_ATTN
   return RCSA_ERR_SHAPE;
+}
+
+// Kernel, then (for a split list) the merge of the partial results.
+template <bool INT8>
+static int launch_attn_split(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
+  int st = launch_attn<INT8>(a, D, BM, BN, s);
+  if (st || a.n_split == 1) return st;
+  const int64_t threads = a.n_bh * a.q_len * (D / 8);
+  const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+  if (D == 128) attn_merge_kernel<128><<<grid, dim3(256), 0, s>>>(a);
+  else attn_merge_kernel<64><<<grid, dim3(256), 0, s>>>(a);
+  return launch_status();
+}
+
+// Workspace of a split launch: normalised bf16 partials, then (m, l) pairs.
+static int64_t ws_o_bytes(int64_t n_bh, int64_t q_len, int64_t d, int64_t n_split) {
+  return ((n_split * n_bh * q_len * d * 2) + 255) / 256 * 256;
+}
+static int64_t ws_bytes(int64_t n_bh, int64_t q_len, int64_t d, int64_t n_split) {
+  return n_split <= 1 ? 0 : ws_o_bytes(n_bh, q_len, d, n_split) + n_split * n_bh * q_len * 8;
+}
+
+static int apply_split(AttnArgs& a, int64_t d, int64_t n_split, void* workspace,
+                       int64_t workspace_bytes) {
+  if (n_split < 1 || n_split > 16) return RCSA_ERR_SHAPE;
+  if (n_split == 1) return RCSA_OK;
+  if (workspace == nullptr) return RCSA_ERR_NULL;
+  if (!aligned16(workspace)) return RCSA_ERR_ALIGN;
+  if (workspace_bytes < ws_bytes(a.n_bh, a.q_len, d, n_split)) return RCSA_ERR_SHAPE;
+  a.n_split = n_split;
+  a.ws_o = static_cast<u16*>(workspace);
+  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
+                                      ws_o_bytes(a.n_bh, a.q_len, d, n_split));
+  a.n_work *= n_split;
+  return RCSA_OK;
 }
 
 static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, float* M,
@@ -588,6 +685,8 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   a.n_qblocks = (Q_LEN + BM - 1) / BM;
   a.n_kblocks = (K_LEN + BN - 1) / BN;
   a.max_k = max_k;
+  a.n_bh = B * H;
+  a.n_split = 1;
   a.n_work = B * H * a.n_qblocks;
   return RCSA_OK;
 }
@@ -596,7 +695,7 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
 
 using namespace rcsa;
 
-extern "C" int rcsa_sparse_attn_bf16(
+extern "C" int rcsa_sparse_attn_bf16_split(
     const void* Q, const void* K, const void* V, const uint8_t* K_valid, float sm_scale,
     float* M, void* Out, const int32_t* block_indices, const int32_t* block_indices_lens,
     int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_kz,
@@ -605,7 +704,7 @@ extern "C" int rcsa_sparse_attn_bf16(
     int64_t stride_bz, int64_t stride_bh, int64_t stride_bm, int64_t stride_lz,
     int64_t stride_lh, int64_t stride_lm, int64_t B, int64_t H, int64_t Q_LEN,
     int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N, int64_t max_k,
-    hipStream_t stream) {
+    int64_t n_split, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   if (!Q || !K || !V) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -618,11 +717,13 @@ extern "C" int rcsa_sparse_attn_bf16(
                        stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B,
                        H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 8);
   if (st) return st;
+  st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
+  if (st) return st;
   if (a.n_work == 0) return RCSA_OK;
-  return launch_attn<false>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
+  return launch_attn_split<false>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
 }
 
-extern "C" int rcsa_sparse_attn_int8(
+extern "C" int rcsa_sparse_attn_int8_split(
     const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
     const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
     float sm_scale, float* M, void* Out, const int32_t* block_indices,
@@ -632,7 +733,8 @@ extern "C" int rcsa_sparse_attn_int8(
     int64_t stride_oh, int64_t stride_om, int64_t stride_bz, int64_t stride_bh,
     int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
-    int64_t BLOCK_N, int64_t max_k, hipStream_t stream) {
+    int64_t BLOCK_N, int64_t max_k, int64_t n_split, void* workspace,
+    int64_t workspace_bytes, hipStream_t stream) {
   if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -650,6 +752,83 @@ extern "C" int rcsa_sparse_attn_int8(
                        H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 16);
   if (st) return st;
   if (q_scale_stride < a.n_qblocks || k_scale_stride < a.n_kblocks) return RCSA_ERR_STRIDE;
+  st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
+  if (st) return st;
   if (a.n_work == 0) return RCSA_OK;
-  return launch_attn<true>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
+  return launch_attn_split<true>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
+}
+
+extern "C" int rcsa_sparse_attn_bf16(
+    const void* Q, const void* K, const void* V, const uint8_t* K_valid, float sm_scale,
+    float* M, void* Out, const int32_t* block_indices, const int32_t* block_indices_lens,
+    int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_kz,
+    int64_t stride_kh, int64_t stride_kn, int64_t stride_vz, int64_t stride_vh,
+    int64_t stride_vn, int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+    int64_t stride_bz, int64_t stride_bh, int64_t stride_bm, int64_t stride_lz,
+    int64_t stride_lh, int64_t stride_lm, int64_t B, int64_t H, int64_t Q_LEN,
+    int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N, int64_t max_k,
+    hipStream_t stream) {
+  return rcsa_sparse_attn_bf16_split(
+      Q, K, V, K_valid, sm_scale, M, Out, block_indices, block_indices_lens, stride_qz,
+      stride_qh, stride_qm, stride_kz, stride_kh, stride_kn, stride_vz, stride_vh, stride_vn,
+      stride_oz, stride_oh, stride_om, stride_bz, stride_bh, stride_bm, stride_lz, stride_lh,
+      stride_lm, B, H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, stream);
+}
+
+extern "C" int rcsa_sparse_attn_int8(
+    const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
+    const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
+    float sm_scale, float* M, void* Out, const int32_t* block_indices,
+    const int32_t* block_indices_lens, int64_t stride_qz, int64_t stride_qh,
+    int64_t stride_qm, int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+    int64_t stride_vz, int64_t stride_vh, int64_t stride_vn, int64_t stride_oz,
+    int64_t stride_oh, int64_t stride_om, int64_t stride_bz, int64_t stride_bh,
+    int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
+    int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
+    int64_t BLOCK_N, int64_t max_k, hipStream_t stream) {
+  return rcsa_sparse_attn_int8_split(
+      Q, q_scale, q_scale_stride, K, k_scale, k_scale_stride, V, K_valid, sm_scale, M, Out,
+      block_indices, block_indices_lens, stride_qz, stride_qh, stride_qm, stride_kz,
+      stride_kh, stride_kn, stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
+      stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B, H, Q_LEN, K_LEN,
+      HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, stream);
+}
+
+extern "C" int64_t rcsa_attn_workspace_bytes(int64_t B, int64_t H, int64_t Q_LEN,
+                                             int64_t HEAD_DIM, int64_t n_split) {
+  if (B <= 0 || H <= 0 || Q_LEN <= 0 || HEAD_DIM <= 0 || n_split < 1) return -1;
+  return ws_bytes(B * H, Q_LEN, HEAD_DIM, n_split);
+}
+
+// Split count for B * H * ceil(Q_LEN / BLOCK_M) work items on the current
+// device: the count in 1..4 that minimises the number of workgroup rounds
+// per unit of work (one attention workgroup fills a compute unit), with a
+// small charge for the merge pass, and keeps at least 4 key blocks per split.
+extern "C" int rcsa_attn_split_plan(int64_t B, int64_t H, int64_t Q_LEN, int64_t BLOCK_M,
+                                    int64_t max_k, int64_t* n_split) {
+  if (!n_split) return RCSA_ERR_NULL;
+  if (B <= 0 || H <= 0 || Q_LEN <= 0 || BLOCK_M <= 0 || max_k < 0) return RCSA_ERR_SHAPE;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    return RCSA_ERR_LAUNCH;
+  // One workgroup per compute unit at a time: a launch of rows*s workgroups
+  // takes ceil(rows*s/cus) rounds, each as long as a share of max_k/s key
+  // blocks plus a fixed cost (Q load, prologue, epilogue, partial write and
+  // merge) worth about kFixedBlocks key blocks, measured over 1..4 shares at
+  // 41..152 blocks per list.  Ties keep the smaller count.
+  constexpr double kFixedBlocks = 7.0;
+  const int64_t rows = B * H * ((Q_LEN + BLOCK_M - 1) / BLOCK_M);
+  int64_t best = 1;
+  double best_cost = 0.0;
+  for (int64_t s = 1; s <= 8; ++s) {
+    if (s > 1 && max_k < 2 * s) break;
+    const int64_t rounds = (rows * s + cus - 1) / cus;
+    const double share = static_cast<double>((max_k + s - 1) / s);
+    const double cost = static_cast<double>(rounds) * (kFixedBlocks + share);
+    if (s == 1 || cost < best_cost * 0.98) { best = s; best_cost = cost; }
+  }
+  *n_split = best;
+  return RCSA_OK;
 }

@@ -6,6 +6,7 @@ stream.  No function reads device memory back to the host.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from typing import Optional
 
@@ -247,17 +248,39 @@ def _attn_common(q, k, v, indices, counts, fn):
         raise ValueError(f"{fn}: indices last dim must be contiguous")
 
 
+def _split_plan(B, H, Lq, D, block_m, max_k, n_split, device, fn):
+    """(n_split, workspace tensor or None, workspace bytes) for a split launch.
+
+    ``n_split=None`` asks the library for the count that fills the device's
+    compute units best (rcsa_attn_split_plan); the workspace holds the
+    partial results that the merge pass combines."""
+    lib = _lib.load()
+    if n_split is None:
+        ns = ctypes.c_int64(1)
+        check(lib.rcsa_attn_split_plan(B, H, Lq, block_m, max_k, ctypes.byref(ns)), fn)
+        n_split = ns.value
+    n_split = int(n_split)
+    if n_split < 1:
+        raise ValueError(f"{fn}: n_split must be >= 1")
+    if n_split == 1:
+        return 1, None, 0
+    nbytes = int(lib.rcsa_attn_workspace_bytes(B, H, Lq, D, n_split))
+    return n_split, torch.empty(nbytes, dtype=torch.uint8, device=device), nbytes
+
+
 def _expand_lists(indices, counts, B, H):
     # the reference expands a [1, 1, N, K] layout over (B, H) (stride 0 views)
     return indices.expand(B, H, -1, -1), counts.expand(B, H, -1)
 
 
 def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block_n=128,
-                     sm_scale=None, return_lse=False, out=None):
+                     sm_scale=None, return_lse=False, out=None, n_split=None):
     """bf16 block-sparse attention; the ``_attn_fwd_bsa_align`` contract.
 
     q/k/v [B, H, L, D] bf16, indices int32 [B|1, H|1, NQB, maxK], counts
     int32 [B|1, H|1, NQB], valid: per key token (K_LEN entries) or None.
+    ``n_split`` splits every block list over that many workgroups (merged
+    afterwards); None picks it from the device's compute-unit count.
     """
     fn = "sparse_attn_bf16"
     _require_cuda(fn, q, k, v, indices, counts)
@@ -274,20 +297,22 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
     lse = torch.empty(B, H, Lq, device=q.device, dtype=torch.float32) if return_lse else None
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
-    st = _lib.load().rcsa_sparse_attn_bf16(
+    ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q.device, fn)
+    st = _lib.load().rcsa_sparse_attn_bf16_split(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(kv), scale, _ptr(lse), out.data_ptr(),
         indices.data_ptr(), counts.data_ptr(),
         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
         indices.stride(0), indices.stride(1), indices.stride(2),
         counts.stride(0), counts.stride(1), counts.stride(2),
-        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], _stream())
+        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _stream())
     check(st, fn)
     return (out, lse) if return_lse else out
 
 
 def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=None, *,
-                     block_m=128, block_n=128, sm_scale=None, return_lse=False, out=None):
+                     block_m=128, block_n=128, sm_scale=None, return_lse=False, out=None,
+                     n_split=None):
     """int8-QK / bf16-PV block-sparse attention over quantiser outputs."""
     fn = "sparse_attn_int8"
     _require_cuda(fn, q_i8, q_scale, k_i8, k_scale, v, indices, counts)
@@ -313,7 +338,8 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         out = torch.empty(B, H, Lq, D, device=q_i8.device, dtype=torch.bfloat16)
     lse = torch.empty(B, H, Lq, device=q_i8.device, dtype=torch.float32) if return_lse else None
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
-    st = _lib.load().rcsa_sparse_attn_int8(
+    ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q_i8.device, fn)
+    st = _lib.load().rcsa_sparse_attn_int8_split(
         q_i8.data_ptr(), q_scale.data_ptr(), q_scale.shape[1], k_i8.data_ptr(),
         k_scale.data_ptr(), k_scale.shape[1], v.data_ptr(), _ptr(kv), scale, _ptr(lse),
         out.data_ptr(), indices.data_ptr(), counts.data_ptr(),
@@ -322,7 +348,7 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
         indices.stride(0), indices.stride(1), indices.stride(2),
         counts.stride(0), counts.stride(1), counts.stride(2),
-        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], _stream())
+        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _stream())
     check(st, fn)
     return (out, lse) if return_lse else out
 

@@ -38,14 +38,16 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    block_size: int, k_select, forced: Optional[torch.Tensor] = None,
                    allowed: Optional[torch.Tensor] = None, int8: bool = True,
                    max_k: Optional[int] = None, sm_scale: Optional[float] = None,
-                   return_lse: bool = False, order: str = "index") -> RCSAResult:
+                   return_lse: bool = False, order: str = "index",
+                   n_split: Optional[int] = None) -> RCSAResult:
     """One RCSA layer call over packed Q/K/V ``[B, H, NB*BS, D]`` (bf16 or fp32).
 
     ``k_select`` is the per-row number of key blocks handed to attention
     (history budget + forced blocks such as the current chunk); ``forced``
     marks blocks that are always kept, ``allowed`` the causal permissions.
     With ``int8`` QK^T runs on int8 MFMA over smoothed per-block quantised
-    Q/K; otherwise on bf16 MFMA.
+    Q/K; otherwise on bf16 MFMA.  ``n_split`` splits every block list over
+    that many workgroups (None: chosen from the device's compute-unit count).
     """
     B, H, Lq, D = q.shape
     Lk = k.shape[2]
@@ -65,14 +67,14 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         res = ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v if v.dtype == torch.bfloat16
                                    else v.to(torch.bfloat16), idx4, cnt3, k_valid,
                                    block_m=bs, block_n=bs, sm_scale=scale,
-                                   return_lse=return_lse)
+                                   return_lse=return_lse, n_split=n_split)
     else:
         k_i8 = k_scale = kmean = None
         qb = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
         kb = k if k.dtype == torch.bfloat16 else k.to(torch.bfloat16)
         vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
         res = ops.sparse_attn_bf16(qb, kb, vb, idx4, cnt3, k_valid, block_m=bs, block_n=bs,
-                                   sm_scale=scale, return_lse=return_lse)
+                                   sm_scale=scale, return_lse=return_lse, n_split=n_split)
     out, lse = res if return_lse else (res, None)
     return RCSAResult(out, idx4, cnt3, score, qhat, khat, lse, q_i8, q_scale, k_i8, k_scale,
                       kmean)

@@ -195,6 +195,65 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
                           int64_t max_k, hipStream_t stream);
 
 /*
+ * Split-list variants of the two attention entry points (same arguments,
+ * then n_split, workspace, workspace_bytes).  No reference counterpart: the
+ * reference launches one program per (query block, B*H).  Every query
+ * block's list is cut into n_split contiguous shares handled by separate
+ * workgroups (more workgroups when B*H*ceil(Q_LEN/BLOCK_M) alone would
+ * leave compute units idle); their normalised partial outputs and (max, sum)
+ * pairs go to the caller's workspace and a second kernel on the same stream
+ * combines them:
+ *   w_s = l_s 2^(m_s - M),  out = sum_s w_s O_s / sum_s w_s.
+ * n_split == 1 is the plain entry point (workspace may be NULL).
+ * workspace: 16-byte aligned, at least rcsa_attn_workspace_bytes(...) bytes.
+ */
+int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
+                                const uint8_t* K_valid, float sm_scale, float* M,
+                                void* Out, const int32_t* block_indices,
+                                const int32_t* block_indices_lens,
+                                int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                                int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+                                int64_t stride_vz, int64_t stride_vh, int64_t stride_vn,
+                                int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                                int64_t stride_bz, int64_t stride_bh, int64_t stride_bm,
+                                int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                                int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
+                                int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
+                                int64_t max_k, int64_t n_split, void* workspace,
+                                int64_t workspace_bytes, hipStream_t stream);
+int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
+                                int64_t q_scale_stride, const int8_t* K,
+                                const float* k_scale, int64_t k_scale_stride,
+                                const void* V, const uint8_t* K_valid, float sm_scale,
+                                float* M, void* Out, const int32_t* block_indices,
+                                const int32_t* block_indices_lens,
+                                int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                                int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+                                int64_t stride_vz, int64_t stride_vh, int64_t stride_vn,
+                                int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                                int64_t stride_bz, int64_t stride_bh, int64_t stride_bm,
+                                int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                                int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
+                                int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
+                                int64_t max_k, int64_t n_split, void* workspace,
+                                int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes of a split launch (0 for n_split == 1, -1 on bad sizes). */
+int64_t rcsa_attn_workspace_bytes(int64_t B, int64_t H, int64_t Q_LEN, int64_t HEAD_DIM,
+                                  int64_t n_split);
+
+/*
+ * Split count in 1..8 for the current device: the one that minimises
+ * ceil(rows*s / compute units) * (7 + ceil(max_k / s)), i.e. workgroup
+ * rounds times the length of one share in key blocks plus a fixed cost of
+ * about 7 blocks per workgroup (rows = B*H*ceil(Q_LEN/BLOCK_M)); a larger
+ * count must win by 2% and keep at least 2 key blocks per share.
+ * Host-only (reads device attributes; no device work).
+ */
+int rcsa_attn_split_plan(int64_t B, int64_t H, int64_t Q_LEN, int64_t BLOCK_M,
+                         int64_t max_k, int64_t* n_split);
+
+/*
  * Gather compact tokens into the packed head-major layout, zeroing invalid
  * slots.  Replaces q[:, flat].transpose(1, 2).contiguous(); q_packed[:, :, ~mask] = 0
  * at P/matrix_curvature_phase_frame_weave.py:5671-5684.

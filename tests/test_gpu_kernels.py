@@ -239,3 +239,55 @@ def test_pack_unpack_roundtrip(dev):
     token_slot[perm] = torch.arange(L)
     back = ops.unpack_tokens(packed, token_slot.to(dev))
     assert torch.equal(back.cpu(), x.to(torch.bfloat16))
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_sparse_attn_split_lists(dev, int8):
+    """Splitting every block list over 2..8 workgroups and merging gives the
+    unsplit result (up to the bf16 rounding of the partials) and the oracle's;
+    rows with an empty list (or fewer blocks than splits) stay exact."""
+    from cast_amd import _lib, ops
+    B, H, D, bs = 1, 3, 128, 128
+    q, k, v, qv, kv = _case(9, H=H, nqb=3, nkb=10, D=D, bs=bs, k_valid_tail=bs // 2 + 5)
+    idx, cnt = _lists((B, H), 3, 10, 10, 21)
+    cnt[0, 0, 0] = 0   # empty list
+    cnt[0, 1, 1] = 1   # fewer blocks than splits
+    qd, kd, vd = q.to(dev), k.to(dev), v.to(dev)
+    if int8:
+        _, q8, qs = ops.pool_query(qd, qv.to(dev), bs, quantize=True)
+        _, ksum, kmin, kmax = ops.pool_key(kd, kv.to(dev), bs, stats=True)
+        k8, ks, _ = ops.quantize_key(kd, kv.to(dev), bs, ksum, kmin, kmax)
+        run = lambda s: ops.sparse_attn_int8(q8, qs, k8, ks, vd, idx.to(dev), cnt.to(dev),  # noqa
+                                             kv.to(dev), return_lse=True, n_split=s)
+    else:
+        run = lambda s: ops.sparse_attn_bf16(qd, kd, vd, idx.to(dev), cnt.to(dev), kv.to(dev),  # noqa
+                                             return_lse=True, n_split=s)
+    base, base_lse = run(1)
+    ref, rlse = orc.sparse_attention(q.float(), k.float(), v.float(), idx, cnt, kv,
+                                     block_m=bs, block_n=bs)
+    fin = torch.isfinite(rlse)
+    for s in (2, 3, 4, 8):
+        out, lse = run(s)
+        _check_out(out, base.float().cpu(), torch.ones(q.shape[2], dtype=torch.bool),
+                   f"split {s} vs unsplit", cos_min=0.99999, max_abs=1e-2, rel=5e-3)
+        _check_out(out, ref, qv, f"split {s} vs oracle")
+        assert torch.equal(torch.isfinite(lse.cpu()), fin)
+        # P is rounded to bf16 at each share's own running max: the sums agree
+        # to the bf16 rounding of P, not bit for bit
+        torch.testing.assert_close(lse.cpu()[fin], base_lse.cpu()[fin], atol=2e-3, rtol=0)
+        assert torch.all(out.cpu()[~fin] == 0)
+    # the workspace is checked before any launch
+    lib = _lib.load()
+    need = lib.rcsa_attn_workspace_bytes(B, H, q.shape[2], D, 3)
+    assert need > 0 and lib.rcsa_attn_workspace_bytes(B, H, q.shape[2], D, 1) == 0
+    small = torch.empty(need - 256, dtype=torch.uint8, device=dev)
+    out = torch.empty_like(qd)
+    idx_d, cnt_d = idx.to(dev), cnt.to(dev)
+    args = [qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), None, 1 / math.sqrt(D), None,
+            out.data_ptr(), idx_d.data_ptr(), cnt_d.data_ptr(), *qd.stride()[:3],
+            *kd.stride()[:3], *vd.stride()[:3], *out.stride()[:3], *idx_d.stride()[:3],
+            *cnt_d.stride(), B, H, q.shape[2], k.shape[2], D, bs, bs, idx.shape[3]]
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.rcsa_sparse_attn_bf16_split(*args, 3, small.data_ptr(), need - 256, stream) == 2
+    assert lib.rcsa_sparse_attn_bf16_split(*args, 3, None, need, stream) == 1
+    torch.cuda.synchronize()
