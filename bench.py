@@ -9,7 +9,9 @@ mean-smoothed, 4 K channels x10 outliers), bf16 V, seeded synthetic data.
 A step is one layer call of the hot path: pooled Q (+ fused int8 Q
 quantiser), pooled K (+ smoothing statistics), block scores, top-k
 selection, int8 K quantiser, block-sparse attention.  Inputs are resident in
-HBM before the timed region.
+HBM before the timed region.  Every timed region follows 40-60 ms of the same
+work (the device's clock ramp after idle), then --warmup steps, then exactly
+--steps timed steps.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5]
 
@@ -18,6 +20,7 @@ prints ONE JSON line.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import math
 import os
@@ -35,11 +38,31 @@ HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_int8_dit_traffic.txt")
 
 
+def _prewarm(fn, min_ms: float = 60.0) -> int:
+    """Run ``fn`` back to back for at least ``min_ms`` of wall time.
+
+    After an idle second the device needs about 30 ms of sustained work to
+    reach its steady clock (the attention kernel runs 800 us on the first
+    launch and 543 us from the 50th on), so every timed region is preceded by
+    this much work of its own kind."""
+    import torch
+    t0 = time.perf_counter()
+    calls = 0
+    while (time.perf_counter() - t0) * 1e3 < min_ms:
+        for _ in range(4):
+            fn()
+        calls += 4
+        torch.cuda.synchronize()
+    return calls
+
+
 def _events_time(fn, iters: int, warmup: int = 3) -> float:
-    """Average milliseconds of ``fn`` on the current stream (HIP events)."""
+    """Average milliseconds of ``fn`` on the current stream (HIP events),
+    after ``warmup`` calls and a pre-warm to the device's steady clock."""
     import torch
     for _ in range(warmup):
         fn()
+    _prewarm(fn, 40.0)
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
@@ -158,14 +181,36 @@ def main() -> int:
         return rcsa_attention(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=bs,
                               k_select=w.k_total, forced=w.forced, int8=True, max_k=max_k)
 
+    # one int8 attention dispatch per step: the timed ones are dispatches
+    # [first_timed, first_timed + steps) of this process (a kernel trace's order)
+    first_timed = _prewarm(step, 60.0) + args.warmup
     for _ in range(args.warmup):
         res = step()
+    # HIP events around the attention entry point of every timed step, on the
+    # stream it launches on (torch's current stream): the roofline's launch time
+    attn_events = []
+    entry = ops.sparse_attn_int8
+
+    def timed_entry(*a, **kw):
+        ev0 = torch.cuda.Event(enable_timing=True)
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev0.record()
+        r_ = entry(*a, **kw)
+        ev1.record()
+        attn_events.append((ev0, ev1))
+        return r_
+
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        res = step()
-    torch.cuda.synchronize()
-    ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    ops.sparse_attn_int8 = timed_entry
+    try:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            res = step()
+        torch.cuda.synchronize()
+        ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
+    finally:
+        ops.sparse_attn_int8 = entry
+    attn_ms = statistics.fmean(a.elapsed_time(b) for a, b in attn_events)
     ops_attn = w.attention_ops(res.indices, res.counts)
     value = ops_attn / (ms_per_step * 1e-3) / 1e12
 
@@ -190,7 +235,6 @@ def main() -> int:
         "sparse_attn_int8": _events_time(lambda: ops.sparse_attn_int8(
             q8, qs, k8, ks, w.v, idx4, cnt3, w.k_valid, block_m=bs, block_n=bs, out=out), iters),
     }
-    attn_ms = stage_ms["sparse_attn_int8"]
     achieved = ops_attn / (attn_ms * 1e-3) / 1e12
     qk_ops = pv_ops = ops_attn / 2
     mixed_floor_ms = (qk_ops / (INT8_PEAK_TOPS * 1e12) + pv_ops / (BF16_PEAK_TFLOPS * 1e12)) * 1e3
@@ -231,7 +275,11 @@ def main() -> int:
                      "avg_launch_ms": attn_ms,
                      "mixed_ceiling_frac": mixed_floor_ms / attn_ms},
     }
-    extras = {"stage_ms": stage_ms, "hbm": hbm_frac, "ms_per_layer_call": ms_per_step}
+    ns_plan = ctypes.c_int64(0)
+    _lib.load().rcsa_attn_split_plan(B, H, Lq, bs, max_k, ctypes.byref(ns_plan))
+    extras = {"stage_ms": stage_ms, "hbm": hbm_frac, "ms_per_layer_call": ms_per_step,
+              "attn_split_plan": ns_plan.value,
+              "attn_timed_dispatches": [first_timed, args.steps]}
 
     if not args.no_extras:
         # bf16-QK attention on the same shape (the drop-in kernel)
@@ -250,26 +298,30 @@ def main() -> int:
         plan = workloads.step_sweep_plan(args.seed)
         layers = [workloads.step_layer_view(w, p) for p in plan]
 
-        def sweep():
-            r = []
-            for lw in layers:
-                r.append(rcsa_attention(lw.q, lw.k, lw.v, lw.q_valid, lw.k_valid,
-                                        block_size=bs, k_select=lw.k_total, forced=lw.forced,
-                                        int8=True, max_k=lw.k_total))
-            return r
+        def layer_call(lw):
+            return rcsa_attention(lw.q, lw.k, lw.v, lw.q_valid, lw.k_valid, block_size=bs,
+                                  k_select=lw.k_total, forced=lw.forced, int8=True,
+                                  max_k=lw.k_total)
 
-        sweep()
+        # warm pass (also counts the ops); the timed passes keep no results, so
+        # every layer reuses the previous layer's buffers
+        sweep_ops = 0.0
+        _prewarm(lambda: layer_call(layers[0]), 40.0)
+        for lw in layers:
+            r = layer_call(lw)
+            sweep_ops += lw.attention_ops(r.indices, r.counts)
+            del r
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         n_sweep = 3
         for _ in range(n_sweep):
-            rs = sweep()
+            for lw in layers:
+                layer_call(lw)
         torch.cuda.synchronize()
         step_ms = (time.perf_counter() - t0) * 1e3 / n_sweep
-        sweep_ops = sum(lw.attention_ops(r.indices, r.counts) for lw, r in zip(layers, rs))
         extras["step_sweep_30_layers"] = {"ms_per_step": step_ms,
                                           "effective_TOPS": sweep_ops / step_ms / 1e9}
-        del layers, rs
+        del layers
 
     line["extras"] = extras
     if not args.no_cpu_baseline:
