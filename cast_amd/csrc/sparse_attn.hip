@@ -27,9 +27,8 @@
 // int->float conversion is free and folds into the exp2 argument's FMA.
 // Softmax is online, fp32, exp2 domain (log2(e) folded into the scale); the
 // running max is only moved when a row's max grows by more than 2^8
-// (rescaling O is skipped otherwise).  Row sums accumulate the bf16-rounded
-// probabilities with v_dot2_f32_bf16, so numerator and denominator use the
-// same P.
+// (rescaling O is skipped otherwise).  Row sums accumulate the fp32
+// probabilities (P is rounded to bf16 only as the PV operand).
 #include <type_traits>
 
 #include "rcsa_common.h"
@@ -117,22 +116,31 @@ __device__ __forceinline__ float pair_max(float v) {
   return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
 }
 
-template <bool INT8, int D, int BM, int BN, int STAGES>
+// Validity bytes of a key block when K_valid is NULL.
+#define RCSA_ONES16 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1
+__device__ uint8_t kAllValid[128] = {RCSA_ONES16, RCSA_ONES16, RCSA_ONES16, RCSA_ONES16,
+                                     RCSA_ONES16, RCSA_ONES16, RCSA_ONES16, RCSA_ONES16};
+#undef RCSA_ONES16
+
+// BNS keys of a block are staged per ring step (BN / BNS steps per selected
+// block); NKH key halves split every staged step between wavefronts.
+template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH>
 struct AttnCfg {
   static constexpr int NRG = BM / 32;            // row groups
-  static constexpr int NW = NRG * 2;             // wavefronts: row group x key half
+  static constexpr int NW = NRG * NKH;           // wavefronts: row group x key half
   static constexpr int NT = NW * 64;             // threads
+  static constexpr int SUB = BN / BNS;           // ring steps per selected block
   static constexpr int KB = INT8 ? 1 : 2;        // bytes per K element
   static constexpr int KROW = D * KB;            // bytes per staged K row
   static constexpr int CPR_K = KROW / 16;
   static constexpr int VROW = D * 2;             // bytes per staged V row
   static constexpr int CPR_V = VROW / 16;
   static constexpr int QSTEPS = INT8 ? D / 32 : D / 16;
-  static constexpr int HK = BN / 2;              // keys per wavefront per block
+  static constexpr int HK = BNS / NKH;           // keys per wavefront per step
   static constexpr int KT = HK / 32;             // 32-key tiles per wavefront
   static constexpr int NDT = D / 32;             // 32-wide head_dim tiles
-  static constexpr int KBYTES = BN * KROW;
-  static constexpr int VBYTES = BN * VROW;
+  static constexpr int KBYTES = BNS * KROW;
+  static constexpr int VBYTES = BNS * VROW;
   static constexpr int BUF = KBYTES + VBYTES;    // one ring slot: K tile then V tile
   static constexpr int KUNITS = KBYTES / 1024;   // 1 KiB direct-to-LDS copies
   static constexpr int VUNITS = VBYTES / 1024;
@@ -148,13 +156,30 @@ struct AttnCfg {
   static_assert(STAGES == 2 || (KUNITS % NW == 0 && VUNITS % NW == 0), "uneven copies");
   static_assert(QSTEPS * 2 == CPR_K, "K chunk layout");
   static_assert(STAGES == 2 || STAGES == 3, "ring depth");
+  static_assert((NKH == 1 || NKH == 2) && HK % 32 == 0 && BN % BNS == 0, "key split");
+  static_assert(BNS <= 256, "validity bytes of one step fit the slot tail");
 };
 
-template <bool INT8, int D, int BM, int BN, int STAGES>
-__global__ void __launch_bounds__(BM * 4)  // == AttnCfg::NT
+// Waves per SIMD the register budget is sized for.  A ring of BNS < BN keys
+// fits two workgroups in one compute unit's LDS, so exactly two waves of
+// each SIMD's share must fit; otherwise the compiler's default range applies
+// (at least the workgroup's own waves per SIMD).
+template <int BN, int BNS, int NKH, int NT>
+constexpr int attn_waves_min() { return BNS < BN ? 2 * NKH : (NT / 256 > 1 ? NT / 256 : 1); }
+template <int BN, int BNS, int NKH>
+constexpr int attn_waves_max() { return BNS < BN ? 2 * NKH : 8; }
+
+template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH>
+__global__ void __launch_bounds__(BM * 2 * NKH)  // == AttnCfg::NT
+__attribute__((amdgpu_waves_per_eu(attn_waves_min<BN, BNS, NKH, BM * 2 * NKH>(),
+                                   attn_waves_max<BN, BNS, NKH>())))
 sparse_attn_kernel(AttnArgs a) {
-  using C = AttnCfg<INT8, D, BM, BN, STAGES>;
+  using C = AttnCfg<INT8, D, BM, BN, STAGES, BNS, NKH>;
   typedef typename std::conditional<INT8, v4i, v8bf>::type OpT;
+  // A 3-slot ring issues its copies between the PV MFMAs, every wavefront
+  // the same kOps copies per ring step (validity bytes included)
+  constexpr bool kDmaInPv = STAGES == 3;
+  constexpr int kOps = C::DMA + (kDmaInPv ? 1 : 0);
   typedef typename std::conditional<INT8, v16i, v16f>::type AccT;
   // Ring slots are separate arrays and the loop is unrolled over them, so
   // the compiler can prove that reads of slot j do not alias the copies in
@@ -162,7 +187,8 @@ sparse_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(1024))) char s_0[C::BUF + 256];
   __shared__ __attribute__((aligned(1024))) char s_1[C::BUF + 256];
   __shared__ __attribute__((aligned(1024))) char s_2[STAGES > 2 ? C::BUF + 256 : 16];
-  __shared__ __attribute__((aligned(16))) char s_m[C::MERGE_IN_SLOTS ? 16 : C::NRG * C::MW * 4];
+  __shared__ __attribute__((aligned(16)))
+  char s_m[NKH == 1 || C::MERGE_IN_SLOTS ? 16 : C::NRG * C::MW * 4];
 
   const int64_t work = xcd_remap(blockIdx.x, a.n_work);
   if (work < 0) return;
@@ -215,6 +241,7 @@ sparse_attn_kernel(AttnArgs a) {
     list += begin;
     cnt = end - begin;
   }
+  const int64_t steps = cnt * C::SUB;  // ring steps of BNS keys
   const char* kbase = static_cast<const char*>(a.k) + (b * a.skz + h * a.skh) * C::KB;
   const char* vbase = reinterpret_cast<const char*>(a.v + b * a.svz + h * a.svh);
   const int64_t klast = a.k_len - 1;
@@ -235,18 +262,63 @@ sparse_attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < C::VUPW; ++i)
     v_lo[i] = static_cast<uint32_t>(v_row(i) * vrow_bytes) + v_col(i);
-  // Copy block n (clamped to 0 when invalid) into a slot.  Rows past k_len
-  // re-read the last row (those keys are masked).  (Named source pointers:
-  // an inline pointer expression as this builtin's source argument makes the
-  // host pass drop the kernel stub.)
-  auto stage = [&](int64_t n, char* dst) __attribute__((always_inline)) {
-    const int64_t key0 = (n < 0 ? 0 : n) * BN;
-    const bool tail = key0 + BN > a.k_len;
+  // Copy step n (BNS keys from key n*BNS; clamped to 0 when invalid) into a
+  // slot.  Rows past k_len re-read the last row (those keys are masked).
+  // (Named source pointers: an inline pointer expression as this builtin's
+  // source argument makes the host pass drop the kernel stub.)
+  // Branch-free variant: every lane offset is min(row, rows_left - 1) *
+  // row_bytes + chunk (24-bit multiply; row strides stay below 16 MiB), so
+  // the copies sit in the caller's basic block between its MFMAs.
+  int k_r[C::KUPW], k_c[C::KUPW], v_r[C::VUPW], v_c[C::VUPW];
+#pragma unroll
+  for (int i = 0; i < C::KUPW; ++i) { k_r[i] = k_row(i); k_c[i] = k_col(i); }
+#pragma unroll
+  for (int i = 0; i < C::VUPW; ++i) { v_r[i] = v_row(i); v_c[i] = v_col(i); }
+  const uint32_t krb = static_cast<uint32_t>(krow_bytes), vrb = static_cast<uint32_t>(vrow_bytes);
+  auto stage_flat = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+    int64_t key0 = (n < 0 ? 0 : n) * BNS;
+    key0 = key0 > klast ? klast : key0;
+    const int64_t left = a.k_len - key0;  // >= 1
+    const uint32_t lim = static_cast<uint32_t>(left < BNS ? left - 1 : BNS - 1);
     const char* kb0 = kbase + key0 * krow_bytes;
     const char* vb0 = vbase + key0 * vrow_bytes;
 #pragma unroll
     for (int i = 0; i < C::KUPW; ++i) {
-      if (wave * C::KUPW + i < C::KUNITS) {  // uniform per wavefront
+      const char* src = kb0 + (__umul24(min(static_cast<uint32_t>(k_r[i]), lim), krb) + k_c[i]);
+      __builtin_amdgcn_global_load_lds(
+          src, RCSA_LDS(void, dst + (wave * C::KUPW + i) * 1024), 16, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < C::VUPW; ++i) {
+      const char* src = vb0 + (__umul24(min(static_cast<uint32_t>(v_r[i]), lim), vrb) + v_c[i]);
+      __builtin_amdgcn_global_load_lds(
+          src, RCSA_LDS(void, dst + C::KBYTES + (wave * C::VUPW + i) * 1024), 16, 0, 0);
+    }
+  };
+  // validity bytes of step n, 4 per lane from every wavefront (lanes 32-63
+  // repeat lanes 0-31 into the tail's unused half); offsets past the
+  // readable range are clamped and stand for keys past K_LEN
+  const uint8_t* kvb = a.kvalid != nullptr ? a.kvalid : kAllValid;
+  const int64_t kv_step = a.kvalid != nullptr ? 1 : 0;
+  const int64_t kv_last = a.kvalid != nullptr ? (a.k_len + 15) / 16 * 16 - 4 : 124;
+  auto stage_valid_flat = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+    static_assert(BNS <= 128, "validity bytes of a step: 32 lanes x 4");
+    int64_t key0 = (n < 0 ? 0 : n) * BNS;
+    key0 = key0 > klast ? klast / 16 * 16 : key0;
+    const int64_t vk0 = key0 * kv_step;
+    const uint32_t vlim = static_cast<uint32_t>(kv_last - vk0 < 124 ? kv_last - vk0 : 124);
+    const char* vsrc = reinterpret_cast<const char*>(kvb) + vk0 +
+                       min(static_cast<uint32_t>(4 * (lane & 31)), vlim);
+    __builtin_amdgcn_global_load_lds(vsrc, RCSA_LDS(void, dst + C::BUF), 4, 0, 0);
+  };
+  auto stage = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+    const int64_t key0 = (n < 0 ? 0 : n) * BNS;
+    const bool tail = key0 + BNS > a.k_len;
+    const char* kb0 = kbase + key0 * krow_bytes;
+    const char* vb0 = vbase + key0 * vrow_bytes;
+#pragma unroll
+    for (int i = 0; i < C::KUPW; ++i) {
+      if (C::KUNITS % C::NW == 0 || wave * C::KUPW + i < C::KUNITS) {  // uniform per wavefront
         const char* src = tail ? kbase + min(key0 + k_row(i), klast) * krow_bytes + k_col(i)
                                : kb0 + k_lo[i];
         __builtin_amdgcn_global_load_lds(
@@ -255,7 +327,7 @@ sparse_attn_kernel(AttnArgs a) {
     }
 #pragma unroll
     for (int i = 0; i < C::VUPW; ++i) {
-      if (wave * C::VUPW + i < C::VUNITS) {
+      if (C::VUNITS % C::NW == 0 || wave * C::VUPW + i < C::VUNITS) {
         const char* src = tail ? vbase + min(key0 + v_row(i), klast) * vrow_bytes + v_col(i)
                                : vb0 + v_lo[i];
         __builtin_amdgcn_global_load_lds(
@@ -263,20 +335,22 @@ sparse_attn_kernel(AttnArgs a) {
       }
     }
   };
-  // Block-list entry `it` (-1 = invalid), a scalar load.
+  // Ring step `it`: step SUB*n + it%SUB of list entry n = list[it / SUB]
+  // (-1 = invalid entry), a scalar load.
   auto block_of = [&](int64_t it) __attribute__((always_inline)) -> int64_t {
-    const int64_t n = ld_const(list + it);
-    return (n >= 0 && n < a.n_kblocks) ? n : -1;
+    const int64_t n = ld_const(list + it / C::SUB);
+    return (n >= 0 && n < a.n_kblocks) ? n * C::SUB + it % C::SUB : -1;
   };
   auto fetch_scale = [&](int64_t n) __attribute__((always_inline)) -> float {
-    return INT8 ? ld_const(a.k_scale + bh * a.k_scale_stride + (n < 0 ? 0 : n)) : 1.0f;
+    return INT8 ? ld_const(a.k_scale + bh * a.k_scale_stride + (n < 0 ? 0 : n / C::SUB))
+                : 1.0f;
   };
-  // The BN validity bytes of a whole block ride along with its copies (BN/16
+  // The BNS validity bytes of a step ride along with its copies (BNS/16
   // lanes of wavefront 0, 16 bytes each) into the slot's 256-byte tail;
   // K_valid is 16-byte aligned and readable up to the next 16-byte boundary.
   auto stage_valid = [&](int64_t n, char* dst) __attribute__((always_inline)) {
-    if (a.kvalid != nullptr && wave == 0 && lane < BN / 16) {
-      const int64_t key0 = (n < 0 ? 0 : n) * BN;
+    if (a.kvalid != nullptr && wave == 0 && lane < BNS / 16) {
+      const int64_t key0 = (n < 0 ? 0 : n) * BNS;
       const int64_t chunk = min(key0 + 16 * lane, (klast / 16) * 16);
       const char* src = reinterpret_cast<const char*>(a.kvalid) + chunk;
       __builtin_amdgcn_global_load_lds(src, RCSA_LDS(void, dst + C::BUF), 16, 0, 0);
@@ -284,7 +358,7 @@ sparse_attn_kernel(AttnArgs a) {
   };
   // validity of this lane's key in the wavefront's half, from the slot tail
   auto key_valid = [&](int64_t n, const char* tile) __attribute__((always_inline)) -> bool {
-    const int64_t key = n * BN + kh * C::HK + lane;
+    const int64_t key = n * BNS + kh * C::HK + lane;
     if (n < 0 || lane >= C::HK || key >= a.k_len) return false;
     return a.kvalid == nullptr || tile[C::BUF + kh * C::HK + lane] != 0;
   };
@@ -321,7 +395,8 @@ sparse_attn_kernel(AttnArgs a) {
   }
 
   // One key block from the slot at `tile`.
-  auto compute = [&](const char* tile, int64_t n, float kscale) __attribute__((always_inline)) {
+  auto compute = [&](const char* tile, int64_t n, float kscale, int64_t n_fill,
+                     char* fill) __attribute__((always_inline)) {
     const uint64_t vmask = __ballot(key_valid(n, tile));
     const bool all_valid = vmask == (~0ull >> (64 - C::HK));
     // ---- S^T = K Q^T: every K operand read is issued before the MFMAs ----
@@ -390,22 +465,26 @@ sparse_attn_kernel(AttnArgs a) {
       m_run = m_new;
     }
     const float bias = -(INT8 ? c * kMagicF : 0.0f) - (m_run == -INFINITY ? 0.0f : m_run);
+    // Row sums add the fp32 exponentials in four independent chains: the
+    // bf16 dot instruction would share the matrix pipe and stall behind the
+    // other wavefront's MFMAs, plain adds issue beside them.
     v8bf p_op[C::KT][2];
+    float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int t = 0; t < C::KT; ++t)
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-          p_op[t][u][jj] =
-              static_cast<__bf16>(__builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + jj], c, bias)));
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          const v2bf pair = {p_op[t][u][2 * jj], p_op[t][u][2 * jj + 1]};
-          const v2bf ones = {static_cast<__bf16>(1.0f), static_cast<__bf16>(1.0f)};
-          l_run = __builtin_amdgcn_fdot2_f32_bf16(pair, ones, l_run, false);
+        for (int jj = 0; jj < 8; ++jj) {
+          const float e = __builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + jj], c, bias));
+          p_op[t][u][jj] = static_cast<__bf16>(e);
+          lsum[jj & 3] += e;
         }
-      }
+    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+    if constexpr (kDmaInPv) {
+      stage_valid_flat(n_fill, fill);
+      stage_flat(n_fill, fill);
+    }
     // ---- O^T += V^T P^T, V^T operand by transposing LDS reads; the reads of
     //      the next 16-key step are in flight during this step's MFMAs ----
     auto v_group = [&](int g, v8bf (&op)[C::NDT]) __attribute__((always_inline)) {
@@ -436,6 +515,8 @@ sparse_attn_kernel(AttnArgs a) {
       for (int dt = 0; dt < C::NDT; ++dt) {
         __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
         if (g + 1 < 2 * C::KT) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+        if (kDmaInPv && g * C::NDT + dt < kOps)
+          __builtin_amdgcn_sched_group_barrier(0x010, 1, 0);
       }
   };
 
@@ -444,17 +525,30 @@ sparse_attn_kernel(AttnArgs a) {
   // loads whose latency hides behind that iteration's compute).
   int64_t n_m[3] = {-1, -1, -1};
   float ks_m[3] = {1.0f, 1.0f, 1.0f};
+  if constexpr (kDmaInPv) {
+    // both prologue steps always copy (step 0 stands in past the list), so
+    // every wavefront has exactly 2 * kOps copies in flight
 #pragma unroll
-  for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
-    if (sidx < cnt) {
+    for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
       char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
-      n_m[sidx] = block_of(sidx);
+      n_m[sidx] = sidx < steps ? block_of(sidx) : -1;
       ks_m[sidx] = fetch_scale(n_m[sidx]);
-      stage_valid(n_m[sidx], dst);
-      stage(n_m[sidx], dst);
+      stage_valid_flat(n_m[sidx], dst);
+      stage_flat(n_m[sidx], dst);
+    }
+  } else {
+#pragma unroll
+    for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
+      if (sidx < steps) {
+        char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
+        n_m[sidx] = block_of(sidx);
+        ks_m[sidx] = fetch_scale(n_m[sidx]);
+        stage_valid(n_m[sidx], dst);
+        stage(n_m[sidx], dst);
+      }
     }
   }
-  int64_t n_pre = STAGES - 1 < cnt ? block_of(STAGES - 1) : -1;  // next block to stage
+  int64_t n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;  // next step to stage
   auto iteration = [&](auto slot_c, int64_t j) __attribute__((always_inline)) {
     constexpr int J = decltype(slot_c)::value;
     constexpr int F = (J + STAGES - 1) % STAGES;  // slot of block j + STAGES - 1
@@ -463,86 +557,108 @@ sparse_attn_kernel(AttnArgs a) {
     // block j's copies are the oldest in flight; the STAGES-2 younger
     // stages may remain (wavefront 0's extra validity copy is waited too),
     // then every wavefront's copies of block j have landed and slot F is free
-    if constexpr (STAGES == 3) {
-      if (j + 1 < cnt) wait_vm_barrier<C::DMA>();
+    if constexpr (kDmaInPv) {
+      wait_vm_barrier<kOps>();  // every step issues kOps copies
+    } else if constexpr (STAGES == 3) {
+      if (j + 1 < steps) wait_vm_barrier<C::DMA>();
       else wait_vm_barrier<0>();
     } else {
       wait_vm_barrier<0>();
     }
-    if (j + STAGES - 1 < cnt) {
-      n_m[F] = n_pre;
-      ks_m[F] = fetch_scale(n_pre);
-      stage_valid(n_pre, fill);
-      stage(n_pre, fill);
-      n_pre = j + STAGES < cnt ? block_of(j + STAGES) : -1;
+    if constexpr (kDmaInPv) {
+      // every iteration copies (a step past the list re-copies step 0 into
+      // the slot it fills, which nobody reads), so every wait counts the
+      // same copies; the K/V copies issue between the PV MFMAs
+      const int64_t nf = n_pre;
+      n_m[F] = nf;
+      ks_m[F] = fetch_scale(nf);
+      n_pre = j + STAGES < steps ? block_of(j + STAGES) : -1;
+      compute(tile, n_m[J], ks_m[J], nf, fill);
+    } else {
+      if (j + STAGES - 1 < steps) {
+        n_m[F] = n_pre;
+        ks_m[F] = fetch_scale(n_pre);
+        stage_valid(n_pre, fill);
+        stage(n_pre, fill);
+        n_pre = j + STAGES < steps ? block_of(j + STAGES) : -1;
+      }
+      compute(tile, n_m[J], ks_m[J], -1, fill);
     }
-    compute(tile, n_m[J], ks_m[J]);
   };
-  for (int64_t j = 0; j < cnt; j += STAGES) {
+  for (int64_t j = 0; j < steps; j += STAGES) {
     iteration(std::integral_constant<int, 0>{}, j);
-    if (j + 1 >= cnt) break;
+    if (j + 1 >= steps) break;
     iteration(std::integral_constant<int, 1>{}, j + 1);
     if constexpr (STAGES > 2) {
-      if (j + 2 >= cnt) break;
+      if (j + 2 >= steps) break;
       iteration(std::integral_constant<int, 2>{}, j + 2);
     }
   }
 
-  // ---- merge the two key halves, normalise, write O (bf16) and the LSE ----
+  // the trailing copies (past the list) land before the slots are reused or freed
+  if constexpr (kDmaInPv) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // ---- merge the key halves, normalise, write O (bf16) and the LSE ----
   const float l_tot = pair_sum(l_run);
-  __syncthreads();  // main loop done everywhere: LDS is free for the merge
-  float* mbuf;
-  if constexpr (C::MERGE_IN_SLOTS) {
-    const int sl = rg % STAGES;
-    mbuf = reinterpret_cast<float*>(sl == 0 ? s_0 : sl == 1 ? s_1 : s_2) +
+  float m = m_run, l = l_tot, fa = 1.0f, fb = 0.0f;
+  const float* mbuf = nullptr;
+  if constexpr (NKH == 2) {
+    __syncthreads();  // main loop done everywhere: LDS is free for the merge
+    float* mb;
+    if constexpr (C::MERGE_IN_SLOTS) {
+      const int sl = rg % STAGES;
+      mb = reinterpret_cast<float*>(sl == 0 ? s_0 : sl == 1 ? s_1 : s_2) +
            (rg / STAGES) * C::MW;
-  } else {
-    mbuf = reinterpret_cast<float*>(s_m) + rg * C::MW;
-  }
-  if (kh == 1) {
-#pragma unroll
-    for (int dt = 0; dt < C::NDT; ++dt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) mbuf[(dt * 16 + r) * 64 + lane] = o_acc[dt][r];
-    mbuf[C::NDT * 16 * 64 + lane] = m_run;
-    mbuf[C::NDT * 16 * 64 + 64 + lane] = l_tot;
-  }
-  __syncthreads();
-  if (kh == 0) {
-    const float m_b = mbuf[C::NDT * 16 * 64 + lane];
-    const float l_b = mbuf[C::NDT * 16 * 64 + 64 + lane];
-    const float m = fmaxf(m_run, m_b);
-    const float wa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
-    const float wb = m_b == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_b - m);
-    const float l = l_tot * wa + l_b * wb;
-    const float inv = l > 0.0f ? 1.0f / l : 0.0f;
-    const float fa = wa * inv, fb = wb * inv;
-    if (qrow_ok) {
-      // a split writes its normalised partial and (m, l) to the workspace
-      const int64_t ws_row = (split * a.n_bh + bh) * a.q_len + qrow;
-      u16* op = a.n_split == 1 ? a.out + b * a.soz + h * a.soh + qrow * a.som
-                               : a.ws_o + ws_row * D;
+    } else {
+      mb = reinterpret_cast<float*>(s_m) + rg * C::MW;
+    }
+    if (kh == 1) {
 #pragma unroll
       for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          float o4[4];
+        for (int r = 0; r < 16; ++r) mb[(dt * 16 + r) * 64 + lane] = o_acc[dt][r];
+      mb[C::NDT * 16 * 64 + lane] = m_run;
+      mb[C::NDT * 16 * 64 + 64 + lane] = l_tot;
+    }
+    __syncthreads();
+    if (kh == 1) return;
+    const float m_b = mb[C::NDT * 16 * 64 + lane];
+    const float l_b = mb[C::NDT * 16 * 64 + 64 + lane];
+    m = fmaxf(m_run, m_b);
+    fa = m_run == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_run - m);
+    fb = m_b == -INFINITY ? 0.0f : __builtin_amdgcn_exp2f(m_b - m);
+    l = l_tot * fa + l_b * fb;
+    mbuf = mb;
+  }
+  const float inv = l > 0.0f ? 1.0f / l : 0.0f;
+  fa *= inv;
+  fb *= inv;
+  if (qrow_ok) {
+    // a split writes its normalised partial and (m, l) to the workspace
+    const int64_t ws_row = (split * a.n_bh + bh) * a.q_len + qrow;
+    u16* op = a.n_split == 1 ? a.out + b * a.soz + h * a.soh + qrow * a.som
+                             : a.ws_o + ws_row * D;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g + e;
-            o4[e] = o_acc[dt][r] * fa + mbuf[(dt * 16 + r) * 64 + lane] * fb;
-          }
-          const int d0 = 32 * dt + 8 * g + 4 * hf;
-          *reinterpret_cast<uint2*>(op + d0) =
-              make_uint2(pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3]));
+    for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        float o4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          o4[e] = o_acc[dt][r] * fa;
+          if constexpr (NKH == 2) o4[e] += mbuf[(dt * 16 + r) * 64 + lane] * fb;
         }
-      if (hf == 0) {
-        if (a.n_split > 1) {
-          a.ws_ml[ws_row] = make_float2(l > 0.0f ? m : -INFINITY, l);
-        } else if (a.lse) {
-          a.lse[(b * a.H + h) * a.q_len + qrow] =
-              l > 0.0f ? (m + __log2f(l)) * 0.69314718055994531f : -INFINITY;
-        }
+        const int d0 = 32 * dt + 8 * g + 4 * hf;
+        *reinterpret_cast<uint2*>(op + d0) =
+            make_uint2(pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3]));
+      }
+    if (hf == 0) {
+      if (a.n_split > 1) {
+        a.ws_ml[ws_row] = make_float2(l > 0.0f ? m : -INFINITY, l);
+      } else if (a.lse) {
+        a.lse[(b * a.H + h) * a.q_len + qrow] =
+            l > 0.0f ? (m + __log2f(l)) * 0.69314718055994531f : -INFINITY;
       }
     }
   }
@@ -593,10 +709,10 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
   const dim3 grid(static_cast<unsigned>(xcd_grid(a.n_work)));
   // int8 at D=128, 128x128 blocks keeps two blocks in flight (3 x 48 KiB);
   // the other shapes double-buffer.
-#define RCSA_ATTN(D_, BM_, BN_, ST_)                                               \
-  if (D == D_ && BM == BM_ && BN == BN_) {                                          \
-    sparse_attn_kernel<INT8, D_, BM_, BN_, ST_><<<grid, dim3(BM_ * 4), 0, s>>>(a);   \
-    return launch_status();                                                         \
+#define RCSA_ATTN(D_, BM_, BN_, ST_)                                                   \
+  if (D == D_ && BM == BM_ && BN == BN_) {                                              \
+    sparse_attn_kernel<INT8, D_, BM_, BN_, ST_, BN_, 2><<<grid, dim3(BM_ * 4), 0, s>>>(a); \
+    return launch_status();                                                             \
   }
   RCSA_ATTN(128, 128, 128, INT8 ? 3 : 2)
   RCSA_ATTN(128, 128, 64, 2)
@@ -662,6 +778,9 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   if (sqm % kvec || sqh % kvec || sqz % kvec) return RCSA_ERR_STRIDE;
   if (skn % kvec || skh % kvec || skz % kvec) return RCSA_ERR_STRIDE;
   if (svn % 8 || svh % 8 || svz % 8) return RCSA_ERR_STRIDE;
+  // copy addressing multiplies row numbers by the row stride in 24 bits
+  if (skn < 0 || svn < 0 || skn * (16 / kvec) >= (1 << 24) || svn * 2 >= (1 << 24))
+    return RCSA_ERR_STRIDE;
   if (som % 4 || soh % 4 || soz % 4) return RCSA_ERR_STRIDE;
   if (reinterpret_cast<uintptr_t>(Out) & 7u) return RCSA_ERR_ALIGN;
   // validity bytes are copied in aligned 16-byte chunks (the chunk holding the

@@ -150,7 +150,8 @@ int rcsa_quantize_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
  * M (nullable) receives the natural-log log-sum-exp of each row
  * (-inf for a row with no admissible key, whose output row is 0).
  * Indices outside [0, ceil(K_LEN/BLOCK_N)) are skipped; lens are clamped to
- * [0, max_k].  Strides are in elements; every *_k / *_bs stride must be 1.
+ * [0, max_k].  Strides are in elements; every *_k / *_bs stride must be 1;
+ * a K or V row (stride_kn, stride_vn) spans less than 16 MiB.
  * HEAD_DIM in {64, 128}; BLOCK_M, BLOCK_N in {64, 128}.
  * Alignment: Q/K/V rows 16-byte aligned, Out 8-byte aligned, K_valid (when
  * not NULL) 16-byte aligned -- it is read in aligned 16-byte chunks, so up

@@ -290,4 +290,12 @@ def test_sparse_attn_split_lists(dev, int8):
     stream = torch.cuda.current_stream().cuda_stream
     assert lib.rcsa_sparse_attn_bf16_split(*args, 3, small.data_ptr(), need - 256, stream) == 2
     assert lib.rcsa_sparse_attn_bf16_split(*args, 3, None, need, stream) == 1
+    # a K row spanning 16 MiB or more is refused before any launch (the copy
+    # addressing multiplies row numbers by the row stride in 24 bits)
+    big = list(args)
+    big[14] = 1 << 23  # stride_kn of bf16 K: 16 MiB rows
+    assert lib.rcsa_sparse_attn_bf16(*big, stream) == 3
+    big = list(args)
+    big[17] = 1 << 23  # stride_vn
+    assert lib.rcsa_sparse_attn_bf16(*big, stream) == 3
     torch.cuda.synchronize()
