@@ -55,11 +55,15 @@ struct AttnArgs {
   int64_t k_scale_stride;
   int64_t sqz, sqh, sqm, skz, skh, skn, svz, svh, svn, soz, soh, som;
   int64_t sbz, sbh, sbm, slz, slh, slm;
-  int64_t H, q_len, k_len, n_qblocks, n_kblocks, max_k, n_work;
-  // split of every block list over n_split workgroups (1 = no split); the
-  // partial results go to ws_o [n_split][B*H][q_len][D] bf16 (normalised) and
-  // ws_ml [n_split][B*H][q_len] (m, l) for attn_merge_kernel
-  int64_t n_split, n_bh;
+  int64_t H, q_len, k_len, n_qblocks, n_kblocks, max_k, block_m;
+  // Work: n_items = B*H*n_qblocks query blocks.  XCD x runs query blocks
+  // [x xcd_items, (x+1) xcd_items): the first xcd_direct whole, the rest
+  // (those that would run in a round leaving compute units idle) in n_split
+  // shares each.  Tail query block t of XCD x has tail index
+  // x (xcd_items - xcd_direct) + t < n_tail; its shares' normalised partial
+  // outputs go to ws_o [n_split][n_tail][block_m][D] (bf16) and their
+  // (max, sum) pairs to ws_ml [n_split][n_tail][block_m] for attn_merge_kernel.
+  int64_t n_bh, n_items, xcd_items, xcd_direct, n_split, n_tail;
   u16* ws_o;
   float2* ws_ml;
 };
@@ -190,13 +194,19 @@ sparse_attn_kernel(AttnArgs a) {
   __shared__ __attribute__((aligned(16)))
   char s_m[NKH == 1 || C::MERGE_IN_SLOTS ? 16 : C::NRG * C::MW * 4];
 
-  const int64_t work = xcd_remap(blockIdx.x, a.n_work);
-  if (work < 0) return;
-  // consecutive work items: the splits of one query block, then the next
-  // query block of the same head (neighbours share an XCD's L2)
-  const int64_t split = work % a.n_split;
-  const int64_t qb = (work / a.n_split) % a.n_qblocks;
-  const int64_t bh = work / (a.n_split * a.n_qblocks);
+  // Workgroups go to the XCDs round-robin: XCD x runs a contiguous run of
+  // query blocks (neighbouring query blocks of a head share its L2), whole
+  // ones first, then the shares of its tail query blocks back to back.
+  const int64_t xcd = blockIdx.x % kNumXcd, slot = blockIdx.x / kNumXcd;
+  const int64_t tailpos = slot - a.xcd_direct;  // >= 0: a share of a tail query block
+  const int64_t nsp = tailpos < 0 ? 1 : a.n_split;
+  const int64_t split = tailpos < 0 ? 0 : tailpos % a.n_split;
+  const int64_t in_xcd = tailpos < 0 ? slot : a.xcd_direct + tailpos / a.n_split;
+  const int64_t item = xcd * a.xcd_items + in_xcd;
+  if (in_xcd >= a.xcd_items || item >= a.n_items) return;
+  const int64_t tail = xcd * (a.xcd_items - a.xcd_direct) + (in_xcd - a.xcd_direct);
+  const int64_t qb = item % a.n_qblocks;
+  const int64_t bh = item / a.n_qblocks;
   const int64_t b = bh / a.H, h = bh % a.H;
 
   const int tid = threadIdx.x;
@@ -237,7 +247,7 @@ sparse_attn_kernel(AttnArgs a) {
   cnt = cnt < 0 ? 0 : (cnt > a.max_k ? a.max_k : cnt);
   const int32_t* list = a.idx + b * a.sbz + h * a.sbh + qb * a.sbm;
   {  // this workgroup's share of the list (shares differ by at most one block)
-    const int64_t begin = cnt * split / a.n_split, end = cnt * (split + 1) / a.n_split;
+    const int64_t begin = cnt * split / nsp, end = cnt * (split + 1) / nsp;
     list += begin;
     cnt = end - begin;
   }
@@ -634,10 +644,9 @@ sparse_attn_kernel(AttnArgs a) {
   fa *= inv;
   fb *= inv;
   if (qrow_ok) {
-    // a split writes its normalised partial and (m, l) to the workspace
-    const int64_t ws_row = (split * a.n_bh + bh) * a.q_len + qrow;
-    u16* op = a.n_split == 1 ? a.out + b * a.soz + h * a.soh + qrow * a.som
-                             : a.ws_o + ws_row * D;
+    // a share writes its normalised partial and (m, l) to the workspace
+    const int64_t ws_row = (split * a.n_tail + tail) * BM + (qrow - qb * BM);
+    u16* op = nsp == 1 ? a.out + b * a.soz + h * a.soh + qrow * a.som : a.ws_o + ws_row * D;
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
@@ -654,7 +663,7 @@ sparse_attn_kernel(AttnArgs a) {
             make_uint2(pack_bf16x2(o4[0], o4[1]), pack_bf16x2(o4[2], o4[3]));
       }
     if (hf == 0) {
-      if (a.n_split > 1) {
+      if (nsp > 1) {
         a.ws_ml[ws_row] = make_float2(l > 0.0f ? m : -INFINITY, l);
       } else if (a.lse) {
         a.lse[(b * a.H + h) * a.q_len + qrow] =
@@ -664,32 +673,37 @@ sparse_attn_kernel(AttnArgs a) {
   }
 }
 
-// Combine the n_split partial results of every query row:
+// Combine the n_split partial results of every row of the tail query blocks:
 //   w_s = l_s 2^(m_s - M),  out = sum_s w_s O_s / sum_s w_s,  lse = ln 2 (M + log2 sum_s w_s)
-// One thread per (row, 8 channels); rows with no admissible key get 0 / -inf.
+// One thread per (tail row, 8 channels); rows with no admissible key get 0 / -inf.
 template <int D>
 __global__ void __launch_bounds__(256)
 attn_merge_kernel(AttnArgs a) {
-  const int64_t n_bh = a.n_bh;
   constexpr int CPR = D / 8;
   const int64_t v = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int64_t rows = n_bh * a.q_len;
+  const int64_t rows = a.n_tail * a.block_m;
   if (v >= rows * CPR) return;
   const int c = static_cast<int>(v % CPR);
-  const int64_t row = v / CPR;  // bh * q_len + qrow
-  const int64_t bh = row / a.q_len, qrow = row % a.q_len;
+  const int64_t trow = v / CPR;  // tail * block_m + row in block
+  const int64_t tail = trow / a.block_m, r = trow % a.block_m;
+  const int64_t per = a.xcd_items - a.xcd_direct;
+  const int64_t item = (tail / per) * a.xcd_items + a.xcd_direct + tail % per;
+  if (item >= a.n_items) return;
+  const int64_t qb = item % a.n_qblocks, bh = item / a.n_qblocks;
+  const int64_t qrow = qb * a.block_m + r;
+  if (qrow >= a.q_len) return;
   float mx = -INFINITY;
-  for (int64_t s = 0; s < a.n_split; ++s) mx = fmaxf(mx, a.ws_ml[s * rows + row].x);
+  for (int64_t s = 0; s < a.n_split; ++s) mx = fmaxf(mx, a.ws_ml[s * rows + trow].x);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float wsum = 0.0f;
   if (mx != -INFINITY) {
     for (int64_t s = 0; s < a.n_split; ++s) {
-      const float2 ml = a.ws_ml[s * rows + row];
+      const float2 ml = a.ws_ml[s * rows + trow];
       if (ml.x == -INFINITY) continue;
       const float w = ml.y * __builtin_amdgcn_exp2f(ml.x - mx);
       wsum += w;
       float o[8];
-      Vec8<u16>::load(a.ws_o + (s * rows + row) * D + c * 8, o);
+      Vec8<u16>::load(a.ws_o + (s * rows + trow) * D + c * 8, o);
 #pragma unroll
       for (int j = 0; j < 8; ++j) acc[j] = fmaf(w, o[j], acc[j]);
     }
@@ -701,12 +715,14 @@ attn_merge_kernel(AttnArgs a) {
       make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
                  pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv));
   if (a.lse && c == 0)
-    a.lse[row] = wsum > 0.0f ? (mx + __log2f(wsum)) * 0.69314718055994531f : -INFINITY;
+    a.lse[bh * a.q_len + qrow] =
+        wsum > 0.0f ? (mx + __log2f(wsum)) * 0.69314718055994531f : -INFINITY;
 }
 
 template <bool INT8>
 static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
-  const dim3 grid(static_cast<unsigned>(xcd_grid(a.n_work)));
+  const int64_t per_xcd = a.xcd_direct + (a.xcd_items - a.xcd_direct) * a.n_split;
+  const dim3 grid(static_cast<unsigned>(kNumXcd * per_xcd));
   // int8 at D=128, 128x128 blocks keeps two blocks in flight (3 x 48 KiB);
   // the other shapes double-buffer.
 #define RCSA_ATTN(D_, BM_, BN_, ST_)                                                   \
@@ -731,33 +747,60 @@ template <bool INT8>
 static int launch_attn_split(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
   int st = launch_attn<INT8>(a, D, BM, BN, s);
   if (st || a.n_split == 1) return st;
-  const int64_t threads = a.n_bh * a.q_len * (D / 8);
+  const int64_t threads = a.n_tail * a.block_m * (D / 8);
   const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
   if (D == 128) attn_merge_kernel<128><<<grid, dim3(256), 0, s>>>(a);
   else attn_merge_kernel<64><<<grid, dim3(256), 0, s>>>(a);
   return launch_status();
 }
 
-// Workspace of a split launch: normalised bf16 partials, then (m, l) pairs.
-static int64_t ws_o_bytes(int64_t n_bh, int64_t q_len, int64_t d, int64_t n_split) {
-  return ((n_split * n_bh * q_len * d * 2) + 255) / 256 * 256;
-}
-static int64_t ws_bytes(int64_t n_bh, int64_t q_len, int64_t d, int64_t n_split) {
-  return n_split <= 1 ? 0 : ws_o_bytes(n_bh, q_len, d, n_split) + n_split * n_bh * q_len * 8;
+// Compute units per XCD of the current device (0 when it cannot be read);
+// one attention workgroup fills a compute unit.
+static int64_t cus_per_xcd() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus < kNumXcd)
+    return 0;
+  return cus / kNumXcd;
 }
 
+// Workspace of a split launch: normalised bf16 partials, then (m, l) pairs,
+// for n_tail tail query blocks of block_m rows.
+static int64_t ws_o_bytes(int64_t n_tail, int64_t block_m, int64_t d, int64_t n_split) {
+  return ((n_split * n_tail * block_m * d * 2) + 255) / 256 * 256;
+}
+// Upper bound for any BLOCK_M in {64, 128}: at most min(8 (cus_per_xcd - 1),
+// items + 7) tail query blocks (items counted at BLOCK_M = 64) of at most
+// 128 rows.
+static int64_t ws_bound(int64_t n_bh, int64_t q_len, int64_t d, int64_t n_split) {
+  if (n_split <= 1) return 0;
+  int64_t tails = n_bh * ((q_len + 63) / 64) + kNumXcd - 1;
+  const int64_t cux = cus_per_xcd();
+  if (cux > 0 && kNumXcd * (cux - 1) < tails) tails = kNumXcd * (cux - 1);
+  return ws_o_bytes(tails, 128, d, n_split) + n_split * tails * 128 * 8;
+}
+
+// Tail query blocks: on each XCD, those past the last full round of its
+// compute units (all of them when one round is not filled).
 static int apply_split(AttnArgs& a, int64_t d, int64_t n_split, void* workspace,
                        int64_t workspace_bytes) {
   if (n_split < 1 || n_split > 16) return RCSA_ERR_SHAPE;
   if (n_split == 1) return RCSA_OK;
   if (workspace == nullptr) return RCSA_ERR_NULL;
   if (!aligned16(workspace)) return RCSA_ERR_ALIGN;
-  if (workspace_bytes < ws_bytes(a.n_bh, a.q_len, d, n_split)) return RCSA_ERR_SHAPE;
+  if (workspace_bytes < ws_bound(a.n_bh, a.q_len, d, n_split)) return RCSA_ERR_SHAPE;
+  const int64_t cux = cus_per_xcd();
+  if (cux <= 0) return RCSA_ERR_LAUNCH;
+  const int64_t p = a.xcd_items;
+  const int64_t direct = p % cux == 0 ? p : p / cux * cux;
+  if (direct == p) return RCSA_OK;  // every round full: nothing to split
+  a.xcd_direct = direct;
   a.n_split = n_split;
+  a.n_tail = kNumXcd * (p - direct);
   a.ws_o = static_cast<u16*>(workspace);
   a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
-                                      ws_o_bytes(a.n_bh, a.q_len, d, n_split));
-  a.n_work *= n_split;
+                                      ws_o_bytes(a.n_tail, a.block_m, d, n_split));
   return RCSA_OK;
 }
 
@@ -804,9 +847,13 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   a.n_qblocks = (Q_LEN + BM - 1) / BM;
   a.n_kblocks = (K_LEN + BN - 1) / BN;
   a.max_k = max_k;
+  a.block_m = BM;
   a.n_bh = B * H;
+  a.n_items = B * H * a.n_qblocks;
+  a.xcd_items = (a.n_items + kNumXcd - 1) / kNumXcd;
+  a.xcd_direct = a.xcd_items;
   a.n_split = 1;
-  a.n_work = B * H * a.n_qblocks;
+  a.n_tail = 0;
   return RCSA_OK;
 }
 
@@ -838,7 +885,7 @@ extern "C" int rcsa_sparse_attn_bf16_split(
   if (st) return st;
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
-  if (a.n_work == 0) return RCSA_OK;
+  if (a.n_items == 0) return RCSA_OK;
   return launch_attn_split<false>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
 }
 
@@ -873,7 +920,7 @@ extern "C" int rcsa_sparse_attn_int8_split(
   if (q_scale_stride < a.n_qblocks || k_scale_stride < a.n_kblocks) return RCSA_ERR_STRIDE;
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
-  if (a.n_work == 0) return RCSA_OK;
+  if (a.n_items == 0) return RCSA_OK;
   return launch_attn_split<true>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
 }
 
@@ -916,36 +963,34 @@ extern "C" int rcsa_sparse_attn_int8(
 extern "C" int64_t rcsa_attn_workspace_bytes(int64_t B, int64_t H, int64_t Q_LEN,
                                              int64_t HEAD_DIM, int64_t n_split) {
   if (B <= 0 || H <= 0 || Q_LEN <= 0 || HEAD_DIM <= 0 || n_split < 1) return -1;
-  return ws_bytes(B * H, Q_LEN, HEAD_DIM, n_split);
+  return ws_bound(B * H, Q_LEN, HEAD_DIM, n_split);
 }
 
-// Split count for B * H * ceil(Q_LEN / BLOCK_M) work items on the current
-// device: the count in 1..4 that minimises the number of workgroup rounds
-// per unit of work (one attention workgroup fills a compute unit), with a
-// small charge for the merge pass, and keeps at least 4 key blocks per split.
+// Split count for B * H * ceil(Q_LEN / BLOCK_M) query blocks on the current
+// device.  Each XCD runs ceil(items / 8) of them on its compute units, one
+// workgroup per unit at a time: `full` whole rounds, then `rem` tail query
+// blocks, which s shares turn into ceil(rem s / units) rounds of
+// ceil(max_k / s) key blocks.  Every round also pays a fixed cost (Q load,
+// prologue, epilogue, partial write and merge) of about kFixedBlocks key
+// blocks, measured over 1..4 shares at 41..152 blocks per list.  A larger
+// count must win by 2% and keep at least 2 key blocks per share.
 extern "C" int rcsa_attn_split_plan(int64_t B, int64_t H, int64_t Q_LEN, int64_t BLOCK_M,
                                     int64_t max_k, int64_t* n_split) {
   if (!n_split) return RCSA_ERR_NULL;
   if (B <= 0 || H <= 0 || Q_LEN <= 0 || BLOCK_M <= 0 || max_k < 0) return RCSA_ERR_SHAPE;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
-      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      cus <= 0)
-    return RCSA_ERR_LAUNCH;
-  // One workgroup per compute unit at a time: a launch of rows*s workgroups
-  // takes ceil(rows*s/cus) rounds, each as long as a share of max_k/s key
-  // blocks plus a fixed cost (Q load, prologue, epilogue, partial write and
-  // merge) worth about kFixedBlocks key blocks, measured over 1..4 shares at
-  // 41..152 blocks per list.  Ties keep the smaller count.
+  const int64_t cux = cus_per_xcd();
+  if (cux <= 0) return RCSA_ERR_LAUNCH;
   constexpr double kFixedBlocks = 7.0;
-  const int64_t rows = B * H * ((Q_LEN + BLOCK_M - 1) / BLOCK_M);
+  const int64_t items = B * H * ((Q_LEN + BLOCK_M - 1) / BLOCK_M);
+  const int64_t p = (items + kNumXcd - 1) / kNumXcd;
+  const int64_t full = p / cux, rem = p % cux;
   int64_t best = 1;
   double best_cost = 0.0;
-  for (int64_t s = 1; s <= 8; ++s) {
+  for (int64_t s = 1; s <= 8 && rem > 0; ++s) {
     if (s > 1 && max_k < 2 * s) break;
-    const int64_t rounds = (rows * s + cus - 1) / cus;
     const double share = static_cast<double>((max_k + s - 1) / s);
-    const double cost = static_cast<double>(rounds) * (kFixedBlocks + share);
+    const double cost = static_cast<double>(full) * (kFixedBlocks + max_k) +
+                        static_cast<double>((rem * s + cux - 1) / cux) * (kFixedBlocks + share);
     if (s == 1 || cost < best_cost * 0.98) { best = s; best_cost = cost; }
   }
   *n_split = best;

@@ -198,14 +198,16 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
 /*
  * Split-list variants of the two attention entry points (same arguments,
  * then n_split, workspace, workspace_bytes).  No reference counterpart: the
- * reference launches one program per (query block, B*H).  Every query
- * block's list is cut into n_split contiguous shares handled by separate
- * workgroups (more workgroups when B*H*ceil(Q_LEN/BLOCK_M) alone would
- * leave compute units idle); their normalised partial outputs and (max, sum)
- * pairs go to the caller's workspace and a second kernel on the same stream
- * combines them:
+ * reference launches one program per (query block, B*H).  The query blocks
+ * are dealt to the device's 8 XCDs in contiguous runs; on each XCD, those
+ * that would run in a last round leaving compute units idle (all of them
+ * when the XCD's blocks do not fill one round) have their lists cut into
+ * n_split contiguous shares handled by separate workgroups.  The shares'
+ * normalised partial outputs and (max, sum) pairs go to the caller's
+ * workspace and a second kernel on the same stream combines them:
  *   w_s = l_s 2^(m_s - M),  out = sum_s w_s O_s / sum_s w_s.
- * n_split == 1 is the plain entry point (workspace may be NULL).
+ * n_split == 1 is the plain entry point (workspace may be NULL); so is any
+ * n_split when every XCD's query blocks fill whole rounds.
  * workspace: 16-byte aligned, at least rcsa_attn_workspace_bytes(...) bytes.
  */
 int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
@@ -239,17 +241,20 @@ int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t max_k, int64_t n_split, void* workspace,
                                 int64_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes of a split launch (0 for n_split == 1, -1 on bad sizes). */
+/* Workspace bytes of a split launch on the current device, an upper bound
+ * for BLOCK_M in {64, 128} (0 for n_split == 1, -1 on bad sizes). */
 int64_t rcsa_attn_workspace_bytes(int64_t B, int64_t H, int64_t Q_LEN, int64_t HEAD_DIM,
                                   int64_t n_split);
 
 /*
- * Split count in 1..8 for the current device: the one that minimises
- * ceil(rows*s / compute units) * (7 + ceil(max_k / s)), i.e. workgroup
- * rounds times the length of one share in key blocks plus a fixed cost of
- * about 7 blocks per workgroup (rows = B*H*ceil(Q_LEN/BLOCK_M)); a larger
- * count must win by 2% and keep at least 2 key blocks per share.
- * Host-only (reads device attributes; no device work).
+ * Split count in 1..8 for the current device.  Each XCD runs
+ * ceil(items / 8) of the items = B*H*ceil(Q_LEN/BLOCK_M) query blocks on its
+ * compute units (U of them): `full` whole rounds, then `rem` tail blocks.
+ * The count s minimises
+ *   full * (7 + max_k) + ceil(rem * s / U) * (7 + ceil(max_k / s)),
+ * i.e. rounds times the key blocks per workgroup plus a fixed cost of
+ * about 7 blocks per workgroup; a larger count must win by 2% and keep at
+ * least 2 key blocks per share.  Host-only (reads device attributes).
  */
 int rcsa_attn_split_plan(int64_t B, int64_t H, int64_t Q_LEN, int64_t BLOCK_M,
                          int64_t max_k, int64_t* n_split);
