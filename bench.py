@@ -165,8 +165,8 @@ def main() -> int:
         out = torch.empty_like(w.q)
         if w.int8:
             fn = lambda: ops.sparse_attn_int8(r.q_i8, r.q_scale, r.k_i8, r.k_scale, w.v,  # noqa
-                                              r.indices, r.counts, w.k_valid, block_m=bs,
-                                              block_n=bs, out=out)
+                                              r.indices, r.counts, None, block_m=bs,
+                                              block_n=bs, out=out, block_mask=r.k_mask)
         else:
             fn = lambda: ops.sparse_attn_bf16(w.q, w.k, w.v, r.indices, r.counts,  # noqa
                                               w.k_valid, block_m=bs, block_n=bs, out=out)
@@ -217,7 +217,8 @@ def main() -> int:
     # ---- per-kernel timings with HIP events on the launch stream ----
     iters = max(10, args.steps)
     qhat, q8, qs = ops.pool_query(w.q, w.q_valid, bs, quantize=True)
-    khat, ksum, kmin, kmax = ops.pool_key(w.k, w.k_valid, bs, stats=True)
+    khat, ksum, kmin, kmax, kmask = ops.pool_key(w.k, w.k_valid, bs, stats=True,
+                                                 block_mask=True)
     score = ops.block_scores(qhat, khat)
     idx, cnt = ops.select_topk(score, w.k_total, forced=w.forced, max_k=max_k)
     k8, ks, km = ops.quantize_key(w.k, w.k_valid, bs, ksum, kmin, kmax)
@@ -226,14 +227,16 @@ def main() -> int:
     out = torch.empty_like(w.q)
     stage_ms = {
         "pool_query_quant": _events_time(lambda: ops.pool_query(w.q, w.q_valid, bs, True), iters),
-        "pool_key_stats": _events_time(lambda: ops.pool_key(w.k, w.k_valid, bs, True), iters),
+        "pool_key_stats": _events_time(lambda: ops.pool_key(w.k, w.k_valid, bs, True, True),
+                                       iters),
         "block_scores": _events_time(lambda: ops.block_scores(qhat, khat), iters),
         "select_topk": _events_time(lambda: ops.select_topk(score, w.k_total, forced=w.forced,
                                                             max_k=max_k), iters),
         "quantize_key": _events_time(lambda: ops.quantize_key(w.k, w.k_valid, bs, ksum, kmin,
                                                               kmax), iters),
         "sparse_attn_int8": _events_time(lambda: ops.sparse_attn_int8(
-            q8, qs, k8, ks, w.v, idx4, cnt3, w.k_valid, block_m=bs, block_n=bs, out=out), iters),
+            q8, qs, k8, ks, w.v, idx4, cnt3, None, block_m=bs, block_n=bs, out=out,
+            block_mask=kmask), iters),
     }
     achieved = ops_attn / (attn_ms * 1e-3) / 1e12
     qk_ops = pv_ops = ops_attn / 2

@@ -22,6 +22,7 @@ struct PoolArgs {
   float* bmax;
   int8_t* x_i8;     // query quantiser output (pool_query only)
   float* x_scale;   // query scales (pool_query only)
+  uint32_t* mask;   // per-block validity bits (pool_key only, may be NULL)
 };
 
 // Block-wide helpers (kPoolThreads = 4 waves).
@@ -129,6 +130,14 @@ pool_kernel(PoolArgs a) {
   if (t < BS) {
     tv = a.valid == nullptr || a.valid[blk * BS + t] != 0;
     s_valid[t] = tv;
+  }
+  // validity bits of the block (every head shares them: head 0 writes)
+  if (!QUANT && a.mask != nullptr && bh == 0 && t < BS) {
+    const uint64_t bits = __ballot(tv);
+    if (lane == 0) {
+      a.mask[blk * (BS / 32) + 2 * wave] = static_cast<uint32_t>(bits);
+      if (BS - 64 * wave > 32) a.mask[blk * (BS / 32) + 2 * wave + 1] = static_cast<uint32_t>(bits >> 32);
+    }
   }
   const int n_valid = __syncthreads_count(tv);
 
@@ -425,7 +434,7 @@ extern "C" int rcsa_pool_query(const void* q, int dtype, int64_t batch,
   if (!aligned16(q) || (q_i8 && (reinterpret_cast<uintptr_t>(q_i8) & 7u)))
     return RCSA_ERR_ALIGN;
   PoolArgs a{q, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, qhat,
-             nullptr, nullptr, nullptr, q_i8, q_scale};
+             nullptr, nullptr, nullptr, q_i8, q_scale, nullptr};
   const int64_t nbh = batch * n_heads;
   if (dtype == RCSA_BF16) {
     if (q_i8) launch_pool<u16, true, false>(a, nbh, block_size, head_dim, stream);
@@ -441,7 +450,8 @@ extern "C" int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_
                              int64_t n_blocks, int64_t block_size, int64_t head_dim,
                              int64_t stride_b, int64_t stride_h, int64_t stride_t,
                              const uint8_t* valid, float* khat, float* ksum,
-                             float* kmin, float* kmax, hipStream_t stream) {
+                             float* kmin, float* kmax, uint32_t* block_mask,
+                             hipStream_t stream) {
   if (!k || !khat) return RCSA_ERR_NULL;
   const bool stats = ksum || kmin || kmax;
   if (stats && !(ksum && kmin && kmax)) return RCSA_ERR_NULL;
@@ -449,8 +459,9 @@ extern "C" int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_
                             stride_b, stride_h, stride_t);
   if (st) return st;
   if (!aligned16(k)) return RCSA_ERR_ALIGN;
+  if (block_mask && (reinterpret_cast<uintptr_t>(block_mask) & 7u)) return RCSA_ERR_ALIGN;
   PoolArgs a{k, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, khat,
-             ksum, kmin, kmax, nullptr, nullptr};
+             ksum, kmin, kmax, nullptr, nullptr, block_mask};
   const int64_t nbh = batch * n_heads;
   if (dtype == RCSA_BF16) {
     if (stats) launch_pool<u16, false, true>(a, nbh, block_size, head_dim, stream);

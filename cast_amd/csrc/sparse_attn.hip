@@ -44,6 +44,7 @@ struct AttnArgs {
   const void* k;
   const u16* v;
   const uint8_t* kvalid;
+  const uint32_t* kmask;  // validity bits per key (32 per word), replaces kvalid
   float scale_log2;  // sm_scale * log2(e)
   float* lse;
   u16* out;
@@ -173,7 +174,7 @@ constexpr int attn_waves_min() { return BNS < BN ? 2 * NKH : (NT / 256 > 1 ? NT 
 template <int BN, int BNS, int NKH>
 constexpr int attn_waves_max() { return BNS < BN ? 2 * NKH : 8; }
 
-template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH>
+template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH, bool MASK>
 __global__ void __launch_bounds__(BM * 2 * NKH)  // == AttnCfg::NT
 __attribute__((amdgpu_waves_per_eu(attn_waves_min<BN, BNS, NKH, BM * 2 * NKH>(),
                                    attn_waves_max<BN, BNS, NKH>())))
@@ -183,7 +184,10 @@ sparse_attn_kernel(AttnArgs a) {
   // A 3-slot ring issues its copies between the PV MFMAs, every wavefront
   // the same kOps copies per ring step (validity bytes included)
   constexpr bool kDmaInPv = STAGES == 3;
-  constexpr int kOps = C::DMA + (kDmaInPv ? 1 : 0);
+  // validity bytes ride along with the copies unless the caller passes the
+  // validity bits (MASK: read with scalar loads instead)
+  constexpr bool kValidCopy = kDmaInPv && !MASK;
+  constexpr int kOps = C::DMA + (kValidCopy ? 1 : 0);
   typedef typename std::conditional<INT8, v16i, v16f>::type AccT;
   // Ring slots are separate arrays and the loop is unrolled over them, so
   // the compiler can prove that reads of slot j do not alias the copies in
@@ -366,6 +370,18 @@ sparse_attn_kernel(AttnArgs a) {
       __builtin_amdgcn_global_load_lds(src, RCSA_LDS(void, dst + C::BUF), 16, 0, 0);
     }
   };
+  // validity of the wavefront's HK keys of step n from the caller's bits
+  // (uniform scalar loads; keys past K_LEN are cleared)
+  auto mask_bits = [&](int64_t n) __attribute__((always_inline)) -> uint64_t {
+    if (n < 0) return 0;
+    const int64_t key0 = n * BNS + kh * C::HK;
+    const uint32_t* w = a.kmask + key0 / 32;
+    uint64_t m = ld_const(w);
+    if constexpr (C::HK == 64) m |= static_cast<uint64_t>(ld_const(w + 1)) << 32;
+    const int64_t left = a.k_len - key0;
+    if (left < C::HK) m &= left <= 0 ? 0ull : ((1ull << left) - 1);
+    return m;
+  };
   // validity of this lane's key in the wavefront's half, from the slot tail
   auto key_valid = [&](int64_t n, const char* tile) __attribute__((always_inline)) -> bool {
     const int64_t key = n * BNS + kh * C::HK + lane;
@@ -407,7 +423,8 @@ sparse_attn_kernel(AttnArgs a) {
   // One key block from the slot at `tile`.
   auto compute = [&](const char* tile, int64_t n, float kscale, int64_t n_fill,
                      char* fill) __attribute__((always_inline)) {
-    const uint64_t vmask = __ballot(key_valid(n, tile));
+    const uint64_t vmask =
+        (MASK || a.kmask != nullptr) ? mask_bits(n) : __ballot(key_valid(n, tile));
     const bool all_valid = vmask == (~0ull >> (64 - C::HK));
     // ---- S^T = K Q^T: every K operand read is issued before the MFMAs ----
     AccT s_acc[C::KT];
@@ -492,7 +509,7 @@ sparse_attn_kernel(AttnArgs a) {
         }
     l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     if constexpr (kDmaInPv) {
-      stage_valid_flat(n_fill, fill);
+      if constexpr (kValidCopy) stage_valid_flat(n_fill, fill);
       stage_flat(n_fill, fill);
     }
     // ---- O^T += V^T P^T, V^T operand by transposing LDS reads; the reads of
@@ -543,7 +560,7 @@ sparse_attn_kernel(AttnArgs a) {
       char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
       n_m[sidx] = sidx < steps ? block_of(sidx) : -1;
       ks_m[sidx] = fetch_scale(n_m[sidx]);
-      stage_valid_flat(n_m[sidx], dst);
+      if constexpr (kValidCopy) stage_valid_flat(n_m[sidx], dst);
       stage_flat(n_m[sidx], dst);
     }
   } else {
@@ -727,8 +744,14 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
   // the other shapes double-buffer.
 #define RCSA_ATTN(D_, BM_, BN_, ST_)                                                   \
   if (D == D_ && BM == BM_ && BN == BN_) {                                              \
-    sparse_attn_kernel<INT8, D_, BM_, BN_, ST_, BN_, 2><<<grid, dim3(BM_ * 4), 0, s>>>(a); \
+    sparse_attn_kernel<INT8, D_, BM_, BN_, ST_, BN_, 2, false><<<grid, dim3(BM_ * 4), 0, s>>>(a); \
     return launch_status();                                                             \
+  }
+  if constexpr (INT8) {  // the validity-bits flavour of the 3-slot ring
+    if (a.kmask != nullptr && D == 128 && BM == 128 && BN == 128) {
+      sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true><<<grid, dim3(512), 0, s>>>(a);
+      return launch_status();
+    }
   }
   RCSA_ATTN(128, 128, 128, INT8 ? 3 : 2)
   RCSA_ATTN(128, 128, 64, 2)
@@ -892,7 +915,8 @@ extern "C" int rcsa_sparse_attn_bf16_split(
 extern "C" int rcsa_sparse_attn_int8_split(
     const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
     const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
-    float sm_scale, float* M, void* Out, const int32_t* block_indices,
+    const uint32_t* K_block_mask, float sm_scale, float* M, void* Out,
+    const int32_t* block_indices,
     const int32_t* block_indices_lens, int64_t stride_qz, int64_t stride_qh,
     int64_t stride_qm, int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
     int64_t stride_vz, int64_t stride_vh, int64_t stride_vn, int64_t stride_oz,
@@ -918,6 +942,11 @@ extern "C" int rcsa_sparse_attn_int8_split(
                        H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 16);
   if (st) return st;
   if (q_scale_stride < a.n_qblocks || k_scale_stride < a.n_kblocks) return RCSA_ERR_STRIDE;
+  if (K_block_mask) {  // the bits replace the validity bytes
+    if (reinterpret_cast<uintptr_t>(K_block_mask) & 3u) return RCSA_ERR_ALIGN;
+    a.kmask = K_block_mask;
+    a.kvalid = nullptr;
+  }
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
   if (a.n_items == 0) return RCSA_OK;
@@ -944,7 +973,8 @@ extern "C" int rcsa_sparse_attn_bf16(
 extern "C" int rcsa_sparse_attn_int8(
     const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
     const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
-    float sm_scale, float* M, void* Out, const int32_t* block_indices,
+    const uint32_t* K_block_mask, float sm_scale, float* M, void* Out,
+    const int32_t* block_indices,
     const int32_t* block_indices_lens, int64_t stride_qz, int64_t stride_qh,
     int64_t stride_qm, int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
     int64_t stride_vz, int64_t stride_vh, int64_t stride_vn, int64_t stride_oz,
@@ -953,7 +983,8 @@ extern "C" int rcsa_sparse_attn_int8(
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
     int64_t BLOCK_N, int64_t max_k, hipStream_t stream) {
   return rcsa_sparse_attn_int8_split(
-      Q, q_scale, q_scale_stride, K, k_scale, k_scale_stride, V, K_valid, sm_scale, M, Out,
+      Q, q_scale, q_scale_stride, K, k_scale, k_scale_stride, V, K_valid, K_block_mask,
+      sm_scale, M, Out,
       block_indices, block_indices_lens, stride_qz, stride_qh, stride_qm, stride_kz,
       stride_kh, stride_kn, stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
       stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B, H, Q_LEN, K_LEN,

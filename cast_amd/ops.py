@@ -99,10 +99,13 @@ def pool_query(q: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
 
 
 def pool_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
-             stats: bool = False):
+             stats: bool = False, block_mask: bool = False):
     """Masked mean-pool + L2-normalise key blocks (+ sum/min/max for the quantiser).
 
     Returns ``(khat, ksum, kmin, kmax)``; the last three are None unless ``stats``.
+    With ``block_mask`` a fifth value follows: the key validity as bits, int32
+    ``[n_blocks, block_size // 32]`` (bit i of word w of block n = token
+    ``n * block_size + 32 w + i``), the form ``sparse_attn_int8`` takes.
     """
     fn = "pool_key"
     _require_cuda(fn, k)
@@ -115,11 +118,13 @@ def pool_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
                             for _ in range(3))
     else:
         ksum = kmin = kmax = None
+    mask = (torch.empty(NB, block_size // 32, device=k.device, dtype=torch.int32)
+            if block_mask else None)
     st = _lib.load().rcsa_pool_key(
         k.data_ptr(), code, B, H, NB, block_size, D, k.stride(0), k.stride(1), k.stride(2),
-        _ptr(v), khat.data_ptr(), _ptr(ksum), _ptr(kmin), _ptr(kmax), _stream())
+        _ptr(v), khat.data_ptr(), _ptr(ksum), _ptr(kmin), _ptr(kmax), _ptr(mask), _stream())
     check(st, fn)
-    return khat, ksum, kmin, kmax
+    return (khat, ksum, kmin, kmax, mask) if block_mask else (khat, ksum, kmin, kmax)
 
 
 def block_scores(qhat: torch.Tensor, khat: torch.Tensor) -> torch.Tensor:
@@ -312,8 +317,12 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
 
 def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=None, *,
                      block_m=128, block_n=128, sm_scale=None, return_lse=False, out=None,
-                     n_split=None):
-    """int8-QK / bf16-PV block-sparse attention over quantiser outputs."""
+                     n_split=None, block_mask=None):
+    """int8-QK / bf16-PV block-sparse attention over quantiser outputs.
+
+    ``block_mask`` (int32 ``[ceil(Lk / block_n), block_n // 32]``, e.g. from
+    ``pool_key(..., block_mask=True)``) gives the key validity as bits and
+    replaces ``valid``."""
     fn = "sparse_attn_int8"
     _require_cuda(fn, q_i8, q_scale, k_i8, k_scale, v, indices, counts)
     _attn_common(q_i8, k_i8, v, indices, counts, fn)
@@ -333,7 +342,15 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
     if q_scale.shape[1] < nqb or k_scale.shape[1] < nkb:
         raise ValueError(f"{fn}: need {nqb} query and {nkb} key scales per head")
     indices, counts = _expand_lists(indices, counts, B, H)
-    kv = _valid_u8(valid, Lk, q_i8.device, fn)
+    if block_mask is not None:
+        if block_mask.dtype != torch.int32 or block_mask.device != q_i8.device \
+                or block_mask.numel() < nkb * (block_n // 32):
+            raise ValueError(f"{fn}: block_mask must be int32 [{nkb}, {block_n // 32}] "
+                             "on the same device")
+        block_mask = block_mask.contiguous()
+        kv = None
+    else:
+        kv = _valid_u8(valid, Lk, q_i8.device, fn)
     if out is None:
         out = torch.empty(B, H, Lq, D, device=q_i8.device, dtype=torch.bfloat16)
     lse = torch.empty(B, H, Lq, device=q_i8.device, dtype=torch.float32) if return_lse else None
@@ -341,7 +358,8 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q_i8.device, fn)
     st = _lib.load().rcsa_sparse_attn_int8_split(
         q_i8.data_ptr(), q_scale.data_ptr(), q_scale.shape[1], k_i8.data_ptr(),
-        k_scale.data_ptr(), k_scale.shape[1], v.data_ptr(), _ptr(kv), scale, _ptr(lse),
+        k_scale.data_ptr(), k_scale.shape[1], v.data_ptr(), _ptr(kv), _ptr(block_mask),
+        scale, _ptr(lse),
         out.data_ptr(), indices.data_ptr(), counts.data_ptr(),
         q_i8.stride(0), q_i8.stride(1), q_i8.stride(2),
         k_i8.stride(0), k_i8.stride(1), k_i8.stride(2),

@@ -31,6 +31,7 @@ class RCSAResult:
     k_i8: Optional[torch.Tensor] = None
     k_scale: Optional[torch.Tensor] = None
     kmean: Optional[torch.Tensor] = None
+    k_mask: Optional[torch.Tensor] = None  # key validity bits (int8 path)
 
 
 def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -53,7 +54,12 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     Lk = k.shape[2]
     bs = block_size
     qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs, quantize=int8)
-    khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs, stats=int8)
+    if int8:  # the validity bits come with the pooling pass
+        khat, ksum, kmin, kmax, k_mask = ops.pool_key(k, k_valid, bs, stats=True,
+                                                      block_mask=True)
+    else:
+        khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs)
+        k_mask = None
     score = ops.block_scores(qhat, khat)
     indices, counts = ops.select_topk(score, k_select, forced=forced, allowed=allowed,
                                       max_k=max_k, order=order)
@@ -65,9 +71,9 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if int8:
         k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax)
         res = ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v if v.dtype == torch.bfloat16
-                                   else v.to(torch.bfloat16), idx4, cnt3, k_valid,
+                                   else v.to(torch.bfloat16), idx4, cnt3, None,
                                    block_m=bs, block_n=bs, sm_scale=scale,
-                                   return_lse=return_lse, n_split=n_split)
+                                   return_lse=return_lse, n_split=n_split, block_mask=k_mask)
     else:
         k_i8 = k_scale = kmean = None
         qb = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
@@ -77,4 +83,4 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                    sm_scale=scale, return_lse=return_lse, n_split=n_split)
     out, lse = res if return_lse else (res, None)
     return RCSAResult(out, idx4, cnt3, score, qhat, khat, lse, q_i8, q_scale, k_i8, k_scale,
-                      kmean)
+                      kmean, k_mask)

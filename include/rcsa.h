@@ -83,12 +83,15 @@ int rcsa_pool_query(const void* q, int dtype, int64_t batch, int64_t n_heads,
  * (each [B*H, n_blocks, head_dim] fp32, all or none):
  *   ksum = sum over valid tokens, kmin/kmax = min/max over valid tokens
  *   (0 for blocks with no valid token).
+ * block_mask (optional, 8-byte aligned): uint32 [n_blocks][block_size / 32],
+ *   bit i of word w of block n = validity of token n*block_size + 32w + i
+ *   (the form rcsa_sparse_attn_int8 reads; no reference counterpart).
  */
 int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
                   int64_t n_blocks, int64_t block_size, int64_t head_dim,
                   int64_t stride_b, int64_t stride_h, int64_t stride_t,
                   const uint8_t* valid, float* khat, float* ksum, float* kmin,
-                  float* kmax, hipStream_t stream);
+                  float* kmax, uint32_t* block_mask, hipStream_t stream);
 
 /*
  * Cosine block scores score[bh, i, j] = <qhat[bh, i], khat[bh, j]>.
@@ -178,11 +181,16 @@ int rcsa_sparse_attn_bf16(const void* Q, const void* K, const void* V,
  *   logits = sm_scale * q_scale[b*H+h, m] * k_scale[b*H+h, n] * (q_i8 . k_i8)
  * q_scale has ceil(Q_LEN/BLOCK_M) entries per head and k_scale
  * ceil(K_LEN/BLOCK_N) entries per head (row strides given).
+ * K_block_mask (optional, 4-byte aligned): the key validity as bits, uint32
+ * [ceil(K_LEN/BLOCK_N)][BLOCK_N / 32] in rcsa_pool_key's block_mask form;
+ * when given it replaces K_valid (which may then be NULL) and the kernel
+ * reads it with scalar loads instead of staging validity bytes.
  */
 int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
                           int64_t q_scale_stride, const int8_t* K,
                           const float* k_scale, int64_t k_scale_stride,
-                          const void* V, const uint8_t* K_valid, float sm_scale,
+                          const void* V, const uint8_t* K_valid,
+                          const uint32_t* K_block_mask, float sm_scale,
                           float* M, void* Out, const int32_t* block_indices,
                           const int32_t* block_indices_lens,
                           int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
@@ -227,7 +235,8 @@ int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
 int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t q_scale_stride, const int8_t* K,
                                 const float* k_scale, int64_t k_scale_stride,
-                                const void* V, const uint8_t* K_valid, float sm_scale,
+                                const void* V, const uint8_t* K_valid,
+                                const uint32_t* K_block_mask, float sm_scale,
                                 float* M, void* Out, const int32_t* block_indices,
                                 const int32_t* block_indices_lens,
                                 int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,

@@ -217,6 +217,44 @@ def test_sparse_attn_int8_ragged_keys(dev, lk):
     torch.testing.assert_close(lse.cpu()[fin], rlse[fin], atol=2e-2, rtol=0)
 
 
+@pytest.mark.parametrize("D,bs,lk", [(128, 128, 10 * 128), (128, 128, 9 * 128 + 37),
+                                     (64, 64, 10 * 64), (128, 64, 10 * 64)])
+def test_sparse_attn_int8_block_mask(dev, D, bs, lk):
+    """Key validity passed as bits (pool_key's block_mask) gives exactly the
+    output of the per-key validity bytes, on the 3-slot kernel (D 128,
+    128 x 128 blocks) and the generic shapes, with a partial last block."""
+    from cast_amd import ops
+    g = torch.Generator().manual_seed(lk + D)
+    B, H, lq = 1, 3, 3 * bs
+    nkb = -(-lk // bs)
+    k = torch.randn(B, H, nkb * bs, D, generator=g).to(torch.bfloat16)
+    kv = torch.rand(nkb * bs, generator=g) < 0.8
+    kv[lk:] = False
+    kv[2 * bs: 3 * bs] = True  # one fully valid block, one fully invalid
+    kv[3 * bs: 4 * bs] = False
+    kd, kvd = k.to(dev), kv.to(dev)
+    _, ksum, kmin, kmax, mask = ops.pool_key(kd, kvd, bs, stats=True, block_mask=True)
+    bits = torch.tensor([(int(mask.cpu().view(-1)[i // 32]) >> (i % 32)) & 1
+                         for i in range(nkb * bs)], dtype=torch.bool)
+    assert torch.equal(bits, kv), "pool_key block_mask"
+    k8, ks, _ = ops.quantize_key(kd, kvd, bs, ksum, kmin, kmax)
+    k8, ks = k8[:, :, :lk].contiguous(), ks
+    q8 = torch.randint(-127, 128, (B, H, lq, D), generator=g, dtype=torch.int8).to(dev)
+    qs = (torch.rand(B * H, lq // bs, generator=g) * 0.02 + 0.005).to(dev)
+    v = torch.randn(B, H, lk, D, generator=g).to(torch.bfloat16).to(dev)
+    idx, cnt = _lists((B, H), lq // bs, nkb, nkb, 17)
+    idx[..., 0] = nkb - 1
+    cnt.clamp_(min=1)
+    idx_d, cnt_d = idx.to(dev), cnt.to(dev)
+    by_bytes, lse_b = ops.sparse_attn_int8(q8, qs, k8, ks, v, idx_d, cnt_d, kvd[:lk],
+                                           block_m=bs, block_n=bs, return_lse=True, n_split=1)
+    by_bits, lse_m = ops.sparse_attn_int8(q8, qs, k8, ks, v, idx_d, cnt_d, None,
+                                          block_m=bs, block_n=bs, return_lse=True, n_split=1,
+                                          block_mask=mask)
+    assert torch.equal(by_bytes.cpu(), by_bits.cpu())
+    assert torch.equal(lse_b.cpu(), lse_m.cpu())
+
+
 def test_pack_unpack_roundtrip(dev):
     from cast_amd import ops
     g = torch.Generator().manual_seed(7)
