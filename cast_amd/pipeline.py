@@ -5,6 +5,11 @@ This is the compute of ``_compact_cwca_attention``
 gather and the unpack, with the reference's torch eager pooling/top-k and
 the external Triton kernel replaced by the HIP kernels of ``librcsa.so``.
 Every launch is stream-ordered; nothing is read back to the host.
+
+Once Q and K are pooled, the block scores and the top-k run on a side
+stream of the same device, beside the key mean and the int8 K on the
+caller's stream; the caller's stream waits for both before the attention.
+The two small latency-bound kernels then overlap the HBM-bound key pass.
 """
 from __future__ import annotations
 
@@ -15,6 +20,18 @@ from typing import Optional
 import torch
 
 from . import ops
+
+_SIDE_STREAMS: dict = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """One side stream per device (default priority), created on first use."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    s = _SIDE_STREAMS.get(idx)
+    if s is None:
+        s = torch.cuda.Stream(device=idx)
+        _SIDE_STREAMS[idx] = s
+    return s
 
 
 @dataclass
@@ -40,7 +57,7 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    allowed: Optional[torch.Tensor] = None, int8: bool = True,
                    max_k: Optional[int] = None, sm_scale: Optional[float] = None,
                    return_lse: bool = False, order: str = "index",
-                   n_split: Optional[int] = None) -> RCSAResult:
+                   n_split: Optional[int] = None, overlap: bool = True) -> RCSAResult:
     """One RCSA layer call over packed Q/K/V ``[B, H, NB*BS, D]`` (bf16 or fp32).
 
     ``k_select`` is the per-row number of key blocks handed to attention
@@ -49,10 +66,22 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     With ``int8`` QK^T runs on int8 MFMA over smoothed per-block quantised
     Q/K; otherwise on bf16 MFMA.  ``n_split`` splits every block list over
     that many workgroups (None: chosen from the device's compute-unit count).
+    ``overlap`` runs the scores and the top-k on a side stream beside the
+    int8 key pass (int8 only; results are identical either way).
     """
     B, H, Lq, D = q.shape
     Lk = k.shape[2]
     bs = block_size
+    main = torch.cuda.current_stream(q.device) if q.is_cuda else None
+    # the bf16 path has no key pass left to overlap with
+    side = _side_stream(q.device) if (overlap and int8 and q.is_cuda) else None
+
+    def on_side(fn):
+        if side is None:
+            return fn()
+        with torch.cuda.stream(side):
+            return fn()
+
     qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs, quantize=int8)
     if int8:  # the validity bits come with the pooling pass
         khat, ksum, kmin, kmax, k_mask = ops.pool_key(k, k_valid, bs, stats=True,
@@ -60,9 +89,15 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     else:
         khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs)
         k_mask = None
-    score = ops.block_scores(qhat, khat)
-    indices, counts = ops.select_topk(score, k_select, forced=forced, allowed=allowed,
-                                      max_k=max_k, order=order)
+    if side is not None:
+        side.wait_stream(main)  # qhat and khat
+
+    def score_and_select():
+        sc = ops.block_scores(qhat, khat)
+        return sc, ops.select_topk(sc, k_select, forced=forced, allowed=allowed,
+                                   max_k=max_k, order=order)
+
+    score, (indices, counts) = on_side(score_and_select)
     nqb = Lq // bs
     idx4 = indices.view(B, H, nqb, -1)
     cnt3 = counts.view(B, H, nqb)
@@ -70,6 +105,13 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     lse = None
     if int8:
         k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax)
+    if side is not None:
+        main.wait_stream(side)  # the selection
+        # No record_stream: the side stream is private to this function and
+        # every use of it starts after a wait on the caller's stream, so memory
+        # freed on either stream is reused only after the other stream's use.
+        # (Each recorded stream would add event packets between the kernels.)
+    if int8:
         res = ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v if v.dtype == torch.bfloat16
                                    else v.to(torch.bfloat16), idx4, cnt3, None,
                                    block_m=bs, block_n=bs, sm_scale=scale,

@@ -131,6 +131,24 @@ def test_c2_int8_layer(dev):
     _check_attn(fx["out_h0_unquantised"], got, "c2 vs fp32 oracle")
 
 
+def test_c2_side_stream_matches_serial(dev):
+    """The query side on its own stream gives the serial call's results bit
+    for bit, over several back-to-back calls without host syncs between."""
+    from cast_amd import workloads
+    from cast_amd.pipeline import rcsa_attention
+    g = workloads.matrix_dit(2, heads=4, int8=True).to(dev)
+    kw = dict(block_size=128, k_select=g.k_total, forced=g.forced, int8=True,
+              return_lse=True)
+    ref = rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, overlap=False, **kw)
+    runs = [rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, overlap=True, **kw)
+            for _ in range(3)]
+    torch.cuda.synchronize()
+    for i, res in enumerate(runs):
+        for name in ("out", "lse", "indices", "counts", "score", "q_i8", "q_scale", "k_i8",
+                     "k_scale", "k_mask"):
+            assert torch.equal(getattr(res, name), getattr(ref, name)), f"call {i}: {name}"
+
+
 def test_c3_selection_stress(dev):
     from cast_amd import ops
     fx = _golden.load("c3_selection")
