@@ -77,9 +77,20 @@ constexpr int kMagicI = 0x4B400000;        // its fp32 bit pattern
 __device__ __forceinline__ int key_perm(int m) {
   return 16 * ((m >> 2) & 1) + 4 * (m >> 3) + (m & 3);
 }
-// 16-byte chunk swizzles (bank-conflict-free ds_read_b128 of permuted K rows,
-// balanced ds_read_b64_tr_b16 over 4-row groups of V).
-__device__ __forceinline__ int swz_k(int row) { return (row & 3) | ((row >> 2) & 4); }
+// 16-byte chunk swizzles.  LDS serves 256 bytes per clock from 64 four-byte
+// banks.  A ds_read_b128 of the K operand serves 16 lanes per clock, which
+// read the permuted rows {0-7, 16-23} (or {8-15, 24-31}, plus 32t and the key
+// half): rows that share a 256-byte bank line (row / (256 / KROW) equal
+// modulo the line) get distinct chunk XORs, so the 16 reads hit 16 distinct
+// 16-byte bank groups.  V rows XOR by 4 * (row mod 4), which keeps the
+// ds_read_b64_tr_b16 groups of 4 rows conflict free.
+template <int KROW>
+__device__ __forceinline__ int swz_k(int row) {
+  constexpr int RPL = 256 / KROW;     // rows per bank line: 1, 2 or 4
+  constexpr int M = KROW / 16 / 2;    // half the chunks of a row
+  const int q = row / RPL;
+  return (q & (M - 1)) | ((q >> 1) & M);
+}
 __device__ __forceinline__ int swz_v(int row) { return 4 * (row & 3); }
 
 // s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding:
@@ -201,17 +212,24 @@ sparse_attn_kernel(AttnArgs a) {
   // Workgroups go to the XCDs round-robin: XCD x runs a contiguous run of
   // query blocks (neighbouring query blocks of a head share its L2), whole
   // ones first, then the shares of its tail query blocks back to back.
-  const int64_t xcd = blockIdx.x % kNumXcd, slot = blockIdx.x / kNumXcd;
-  const int64_t tailpos = slot - a.xcd_direct;  // >= 0: a share of a tail query block
-  const int64_t nsp = tailpos < 0 ? 1 : a.n_split;
-  const int64_t split = tailpos < 0 ? 0 : tailpos % a.n_split;
-  const int64_t in_xcd = tailpos < 0 ? slot : a.xcd_direct + tailpos / a.n_split;
-  const int64_t item = xcd * a.xcd_items + in_xcd;
-  if (in_xcd >= a.xcd_items || item >= a.n_items) return;
-  const int64_t tail = xcd * (a.xcd_items - a.xcd_direct) + (in_xcd - a.xcd_direct);
-  const int64_t qb = item % a.n_qblocks;
-  const int64_t bh = item / a.n_qblocks;
-  const int64_t b = bh / a.H, h = bh % a.H;
+  // (32-bit decode: the host keeps work items below 2^31)
+  const uint32_t xcd = blockIdx.x % kNumXcd, slot = blockIdx.x / kNumXcd;
+  const uint32_t x_items = static_cast<uint32_t>(a.xcd_items);
+  const uint32_t x_direct = static_cast<uint32_t>(a.xcd_direct);
+  const bool is_share = slot >= x_direct;  // a share of a tail query block
+  const uint32_t tailpos = slot - x_direct;
+  const uint32_t nsp = is_share ? static_cast<uint32_t>(a.n_split) : 1u;
+  const uint32_t split = is_share ? tailpos % nsp : 0u;
+  const uint32_t in_xcd = is_share ? x_direct + tailpos / nsp : slot;
+  const uint32_t item = xcd * x_items + in_xcd;
+  if (in_xcd >= x_items || item >= static_cast<uint32_t>(a.n_items)) return;
+  const int64_t tail = static_cast<int64_t>(xcd) * (x_items - x_direct) +
+                       (static_cast<int64_t>(in_xcd) - x_direct);
+  const uint32_t nqb32 = static_cast<uint32_t>(a.n_qblocks), h32 = static_cast<uint32_t>(a.H);
+  const int64_t qb = item % nqb32;
+  const uint32_t bh32 = item / nqb32;
+  const int64_t bh = bh32;
+  const int64_t b = bh32 / h32, h = bh32 % h32;
 
   const int tid = threadIdx.x;
   const int lane = tid % kWave;
@@ -220,6 +238,11 @@ sparse_attn_kernel(AttnArgs a) {
   const int hf = lane >> 5, lr = lane & 31;
   const int64_t qrow = qb * BM + rg * 32 + lr;
   const bool qrow_ok = qrow < a.q_len;
+
+  // Workgroup-uniform list length and query-block scale, through the scalar
+  // cache, issued ahead of the Q loads so the two latencies overlap.
+  int64_t cnt = ld_const(a.lens + (b * a.slz + h * a.slh + qb * a.slm));
+  const float qs = INT8 ? ld_const(a.q_scale + (bh * a.q_scale_stride + qb)) : 1.0f;
 
   // Q operand (B of S^T = K Q^T): lane half hf holds the row's bytes
   // [hf*KROW/2, (hf+1)*KROW/2) as QSTEPS 16-byte steps.
@@ -234,10 +257,11 @@ sparse_attn_kernel(AttnArgs a) {
       q_op[st] = __builtin_bit_cast(OpT, raw);
     }
   }
-  const float qs = INT8 ? a.q_scale[bh * a.q_scale_stride + qb] : 1.0f;
   // Q must be resident before the ring starts: otherwise its pending loads
-  // meet the loop's back edge and the compiler drains at the first MFMA
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  // meet the loop's back edge and the compiler drains at the first MFMA.
+  // A 3-slot ring waits for them after issuing its two prologue stages
+  // (counted below); the other rings wait here.
+  if constexpr (!kDmaInPv) __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
 
   v16f o_acc[C::NDT];
 #pragma unroll
@@ -247,11 +271,12 @@ sparse_attn_kernel(AttnArgs a) {
   float m_run = -INFINITY;  // running max (log2 domain), shared by both lane halves
   float l_run = 0.0f;       // this lane's partial row sum
 
-  int64_t cnt = a.lens[b * a.slz + h * a.slh + qb * a.slm];
   cnt = cnt < 0 ? 0 : (cnt > a.max_k ? a.max_k : cnt);
   const int32_t* list = a.idx + b * a.sbz + h * a.sbh + qb * a.sbm;
   {  // this workgroup's share of the list (shares differ by at most one block)
-    const int64_t begin = cnt * split / nsp, end = cnt * (split + 1) / nsp;
+    // (cnt < 2^24 and split < 16: the products fit in 32 bits)
+    const uint32_t c32 = static_cast<uint32_t>(cnt);
+    const int64_t begin = c32 * split / nsp, end = c32 * (split + 1) / nsp;
     list += begin;
     cnt = end - begin;
   }
@@ -267,7 +292,7 @@ sparse_attn_kernel(AttnArgs a) {
   // plus a loop-invariant 32-bit lane offset.
   auto k_row = [&](int i) __attribute__((always_inline)) { return (wave * C::KUPW + i) * C::K_RPU + lane / C::CPR_K; };
   auto v_row = [&](int i) __attribute__((always_inline)) { return (wave * C::VUPW + i) * C::V_RPU + lane / C::CPR_V; };
-  auto k_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_K) ^ (swz_k(k_row(i)) & (C::CPR_K - 1))) * 16; };
+  auto k_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_K) ^ (swz_k<C::KROW>(k_row(i)) & (C::CPR_K - 1))) * 16; };
   auto v_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_V) ^ (swz_v(v_row(i)) & (C::CPR_V - 1))) * 16; };
   uint32_t k_lo[C::KUPW], v_lo[C::VUPW];
 #pragma unroll
@@ -351,9 +376,11 @@ sparse_attn_kernel(AttnArgs a) {
   };
   // Ring step `it`: step SUB*n + it%SUB of list entry n = list[it / SUB]
   // (-1 = invalid entry), a scalar load.
-  auto block_of = [&](int64_t it) __attribute__((always_inline)) -> int64_t {
-    const int64_t n = ld_const(list + it / C::SUB);
+  auto block_step = [&](int64_t n, int64_t it) __attribute__((always_inline)) -> int64_t {
     return (n >= 0 && n < a.n_kblocks) ? n * C::SUB + it % C::SUB : -1;
+  };
+  auto block_of = [&](int64_t it) __attribute__((always_inline)) -> int64_t {
+    return block_step(ld_const(list + it / C::SUB), it);
   };
   auto fetch_scale = [&](int64_t n) __attribute__((always_inline)) -> float {
     return INT8 ? ld_const(a.k_scale + bh * a.k_scale_stride + (n < 0 ? 0 : n / C::SUB))
@@ -372,15 +399,21 @@ sparse_attn_kernel(AttnArgs a) {
   };
   // validity of the wavefront's HK keys of step n from the caller's bits
   // (uniform scalar loads; keys past K_LEN are cleared)
-  auto mask_bits = [&](int64_t n) __attribute__((always_inline)) -> uint64_t {
+  // (split in two: the raw words, loaded ahead, and the mask of step n)
+  auto mask_words = [&](int64_t n) __attribute__((always_inline)) -> uint2 {
+    const uint32_t* w = a.kmask + ((n < 0 ? 0 : n) * BNS + kh * C::HK) / 32;
+    return make_uint2(ld_const(w), C::HK == 64 ? ld_const(w + 1) : 0u);
+  };
+  auto mask_of = [&](int64_t n, uint2 words) __attribute__((always_inline)) -> uint64_t {
     if (n < 0) return 0;
     const int64_t key0 = n * BNS + kh * C::HK;
-    const uint32_t* w = a.kmask + key0 / 32;
-    uint64_t m = ld_const(w);
-    if constexpr (C::HK == 64) m |= static_cast<uint64_t>(ld_const(w + 1)) << 32;
+    uint64_t m = words.x | (static_cast<uint64_t>(words.y) << 32);
     const int64_t left = a.k_len - key0;
     if (left < C::HK) m &= left <= 0 ? 0ull : ((1ull << left) - 1);
     return m;
+  };
+  auto mask_bits = [&](int64_t n) __attribute__((always_inline)) -> uint64_t {
+    return mask_of(n, mask_words(n));
   };
   // validity of this lane's key in the wavefront's half, from the slot tail
   auto key_valid = [&](int64_t n, const char* tile) __attribute__((always_inline)) -> bool {
@@ -394,7 +427,7 @@ sparse_attn_kernel(AttnArgs a) {
   int k_off[C::QSTEPS];
   {
     const int row = kh * C::HK + key_perm(lr);  // + 32t
-    const int sw = swz_k(row) & (C::CPR_K - 1);
+    const int sw = swz_k<C::KROW>(row) & (C::CPR_K - 1);
 #pragma unroll
     for (int st = 0; st < C::QSTEPS; ++st)
       k_off[st] = row * C::KROW + (((hf * C::QSTEPS + st) ^ sw) * 16);
@@ -420,11 +453,14 @@ sparse_attn_kernel(AttnArgs a) {
     else c_init[r] = 0.0f;
   }
 
-  // One key block from the slot at `tile`.
-  auto compute = [&](const char* tile, int64_t n, float kscale, int64_t n_fill,
-                     char* fill) __attribute__((always_inline)) {
+  // One key block from the slot at `tile`.  `bits` is its key-validity mask
+  // when the caller passes validity bits; `prefetch` issues scalar loads for
+  // later blocks once this block's QK MFMAs are issued (scalar loads return
+  // out of order, so any LDS wait behind them waits for them too).
+  auto compute = [&](const char* tile, int64_t n, float kscale, uint64_t bits, int64_t n_fill,
+                     char* fill, auto&& prefetch) __attribute__((always_inline)) {
     const uint64_t vmask =
-        (MASK || a.kmask != nullptr) ? mask_bits(n) : __ballot(key_valid(n, tile));
+        (MASK || a.kmask != nullptr) ? bits : __ballot(key_valid(n, tile));
     const bool all_valid = vmask == (~0ull >> (64 - C::HK));
     // ---- S^T = K Q^T: every K operand read is issued before the MFMAs ----
     AccT s_acc[C::KT];
@@ -449,6 +485,8 @@ sparse_attn_kernel(AttnArgs a) {
       }
     __builtin_amdgcn_sched_group_barrier(0x100, C::KT * C::QSTEPS, 0);
     __builtin_amdgcn_sched_group_barrier(0x008, C::KT * C::QSTEPS, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch();
     // ---- online softmax: lane half hf, register r <-> key 32t + 16hf + r ----
     // raw value: int8 -> 1.5*2^23 + x read as fp32; bf16 -> the fp32 logit.
     // A masked key's raw value becomes -inf, so max and exp2 need no mask.
@@ -552,6 +590,8 @@ sparse_attn_kernel(AttnArgs a) {
   // loads whose latency hides behind that iteration's compute).
   int64_t n_m[3] = {-1, -1, -1};
   float ks_m[3] = {1.0f, 1.0f, 1.0f};
+  uint2 mk_m[3] = {};  // raw validity words per slot (caller's bits only)
+  const bool use_bits = MASK || a.kmask != nullptr;
   if constexpr (kDmaInPv) {
     // both prologue steps always copy (step 0 stands in past the list), so
     // every wavefront has exactly 2 * kOps copies in flight
@@ -563,6 +603,10 @@ sparse_attn_kernel(AttnArgs a) {
       if constexpr (kValidCopy) stage_valid_flat(n_m[sidx], dst);
       stage_flat(n_m[sidx], dst);
     }
+    if (use_bits) mk_m[0] = mask_words(n_m[0]);
+    // the Q loads precede these 2 * kOps copies: with at most that many
+    // outstanding, Q has landed and both prologue stages stay in flight
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOps));
   } else {
 #pragma unroll
     for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
@@ -576,6 +620,10 @@ sparse_attn_kernel(AttnArgs a) {
     }
   }
   int64_t n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;  // next step to stage
+  // 3-slot ring: the list entry of the step after n_pre, as loaded
+  // (read only when the list is not empty: an empty list may have no entries)
+  int32_t pre_raw =
+      (kDmaInPv && steps > 0) ? ld_const(list + (STAGES < steps ? STAGES : 0) / C::SUB) : -1;
   auto iteration = [&](auto slot_c, int64_t j) __attribute__((always_inline)) {
     constexpr int J = decltype(slot_c)::value;
     constexpr int F = (J + STAGES - 1) % STAGES;  // slot of block j + STAGES - 1
@@ -596,11 +644,22 @@ sparse_attn_kernel(AttnArgs a) {
       // every iteration copies (a step past the list re-copies step 0 into
       // the slot it fills, which nobody reads), so every wait counts the
       // same copies; the K/V copies issue between the PV MFMAs
+      // Scalar loads for later blocks go out after this block's QK MFMAs:
+      // the scale of block j+2, the list entry of block j+3 and the
+      // validity bits of block j+1.
+      // Loaded values are only stored here (their first use is a later
+      // block's), so no wait lands before this block's softmax.
+      constexpr int N1 = (J + 1) % STAGES;  // slot of block j + 1
       const int64_t nf = n_pre;
       n_m[F] = nf;
-      ks_m[F] = fetch_scale(nf);
-      n_pre = j + STAGES < steps ? block_of(j + STAGES) : -1;
-      compute(tile, n_m[J], ks_m[J], nf, fill);
+      n_pre = j + STAGES < steps ? block_step(pre_raw, j + STAGES) : -1;
+      const int64_t nxt = j + STAGES + 1 < steps ? j + STAGES + 1 : 0;  // in-bounds entry
+      compute(tile, n_m[J], ks_m[J], use_bits ? mask_of(n_m[J], mk_m[J]) : 0ull, nf, fill,
+              [&]() __attribute__((always_inline)) {
+                ks_m[F] = fetch_scale(nf);
+                pre_raw = ld_const(list + nxt / C::SUB);
+                if (use_bits) mk_m[N1] = mask_words(n_m[N1]);
+              });
     } else {
       if (j + STAGES - 1 < steps) {
         n_m[F] = n_pre;
@@ -609,7 +668,8 @@ sparse_attn_kernel(AttnArgs a) {
         stage(n_pre, fill);
         n_pre = j + STAGES < steps ? block_of(j + STAGES) : -1;
       }
-      compute(tile, n_m[J], ks_m[J], -1, fill);
+      compute(tile, n_m[J], ks_m[J], use_bits ? mask_bits(n_m[J]) : 0ull, -1, fill,
+              []() __attribute__((always_inline)) {});
     }
   };
   for (int64_t j = 0; j < steps; j += STAGES) {
@@ -873,6 +933,8 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   a.block_m = BM;
   a.n_bh = B * H;
   a.n_items = B * H * a.n_qblocks;
+  // the kernel decodes work items and list shares in 32-bit arithmetic
+  if (a.n_items >= (int64_t{1} << 31) || max_k >= (int64_t{1} << 24)) return RCSA_ERR_SHAPE;
   a.xcd_items = (a.n_items + kNumXcd - 1) / kNumXcd;
   a.xcd_direct = a.xcd_items;
   a.n_split = 1;
