@@ -280,10 +280,13 @@ sparse_attn_kernel(AttnArgs a) {
     list += begin;
     cnt = end - begin;
   }
-  const int64_t steps = cnt * C::SUB;  // ring steps of BNS keys
+  const int steps = static_cast<int>(cnt) * C::SUB;  // ring steps of BNS keys
   const char* kbase = static_cast<const char*>(a.k) + (b * a.skz + h * a.skh) * C::KB;
   const char* vbase = reinterpret_cast<const char*>(a.v + b * a.svz + h * a.svh);
-  const int64_t klast = a.k_len - 1;
+  // Key and block numbers are 32-bit (the host keeps K_LEN below 2^31), so
+  // the per-block scalar arithmetic stays on the scalar unit.
+  const int klen = static_cast<int>(a.k_len), klast = klen - 1;
+  const int nkb = static_cast<int>(a.n_kblocks);
   const int64_t krow_bytes = a.skn * C::KB, vrow_bytes = a.svn * 2;
 
   // Direct-to-LDS staging: copy u of a K (V) tile holds K_RPU (V_RPU) rows;
@@ -314,22 +317,27 @@ sparse_attn_kernel(AttnArgs a) {
 #pragma unroll
   for (int i = 0; i < C::VUPW; ++i) { v_r[i] = v_row(i); v_c[i] = v_col(i); }
   const uint32_t krb = static_cast<uint32_t>(krow_bytes), vrb = static_cast<uint32_t>(vrow_bytes);
-  auto stage_flat = [&](int64_t n, char* dst) __attribute__((always_inline)) {
-    int64_t key0 = (n < 0 ? 0 : n) * BNS;
+  auto stage_flat = [&](int n, char* dst) __attribute__((always_inline)) {
+    int key0 = (n < 0 ? 0 : n) * BNS;
     key0 = key0 > klast ? klast : key0;
-    const int64_t left = a.k_len - key0;  // >= 1
+    const int left = klen - key0;  // >= 1
     const uint32_t lim = static_cast<uint32_t>(left < BNS ? left - 1 : BNS - 1);
-    const char* kb0 = kbase + key0 * krow_bytes;
-    const char* vb0 = vbase + key0 * vrow_bytes;
+    const char* kb0 = kbase + static_cast<int64_t>(key0) * krow_bytes;
+    const char* vb0 = vbase + static_cast<int64_t>(key0) * vrow_bytes;
 #pragma unroll
     for (int i = 0; i < C::KUPW; ++i) {
-      const char* src = kb0 + (__umul24(min(static_cast<uint32_t>(k_r[i]), lim), krb) + k_c[i]);
+      // uniform base + zero-extended 32-bit lane offset: the SGPR-base form
+      const uint32_t off = __umul24(min(static_cast<uint32_t>(k_r[i]), lim), krb) +
+                           static_cast<uint32_t>(k_c[i]);
+      const char* src = kb0 + off;
       __builtin_amdgcn_global_load_lds(
           src, RCSA_LDS(void, dst + (wave * C::KUPW + i) * 1024), 16, 0, 0);
     }
 #pragma unroll
     for (int i = 0; i < C::VUPW; ++i) {
-      const char* src = vb0 + (__umul24(min(static_cast<uint32_t>(v_r[i]), lim), vrb) + v_c[i]);
+      const uint32_t off = __umul24(min(static_cast<uint32_t>(v_r[i]), lim), vrb) +
+                           static_cast<uint32_t>(v_c[i]);
+      const char* src = vb0 + off;
       __builtin_amdgcn_global_load_lds(
           src, RCSA_LDS(void, dst + C::KBYTES + (wave * C::VUPW + i) * 1024), 16, 0, 0);
     }
@@ -340,9 +348,9 @@ sparse_attn_kernel(AttnArgs a) {
   const uint8_t* kvb = a.kvalid != nullptr ? a.kvalid : kAllValid;
   const int64_t kv_step = a.kvalid != nullptr ? 1 : 0;
   const int64_t kv_last = a.kvalid != nullptr ? (a.k_len + 15) / 16 * 16 - 4 : 124;
-  auto stage_valid_flat = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+  auto stage_valid_flat = [&](int n, char* dst) __attribute__((always_inline)) {
     static_assert(BNS <= 128, "validity bytes of a step: 32 lanes x 4");
-    int64_t key0 = (n < 0 ? 0 : n) * BNS;
+    int64_t key0 = static_cast<int64_t>(n < 0 ? 0 : n) * BNS;
     key0 = key0 > klast ? klast / 16 * 16 : key0;
     const int64_t vk0 = key0 * kv_step;
     const uint32_t vlim = static_cast<uint32_t>(kv_last - vk0 < 124 ? kv_last - vk0 : 124);
@@ -350,15 +358,15 @@ sparse_attn_kernel(AttnArgs a) {
                        min(static_cast<uint32_t>(4 * (lane & 31)), vlim);
     __builtin_amdgcn_global_load_lds(vsrc, RCSA_LDS(void, dst + C::BUF), 4, 0, 0);
   };
-  auto stage = [&](int64_t n, char* dst) __attribute__((always_inline)) {
-    const int64_t key0 = (n < 0 ? 0 : n) * BNS;
+  auto stage = [&](int n, char* dst) __attribute__((always_inline)) {
+    const int64_t key0 = static_cast<int64_t>(n < 0 ? 0 : n) * BNS;
     const bool tail = key0 + BNS > a.k_len;
     const char* kb0 = kbase + key0 * krow_bytes;
     const char* vb0 = vbase + key0 * vrow_bytes;
 #pragma unroll
     for (int i = 0; i < C::KUPW; ++i) {
       if (C::KUNITS % C::NW == 0 || wave * C::KUPW + i < C::KUNITS) {  // uniform per wavefront
-        const char* src = tail ? kbase + min(key0 + k_row(i), klast) * krow_bytes + k_col(i)
+        const char* src = tail ? kbase + min(key0 + k_row(i), int64_t{klast}) * krow_bytes + k_col(i)
                                : kb0 + k_lo[i];
         __builtin_amdgcn_global_load_lds(
             src, RCSA_LDS(void, dst + (wave * C::KUPW + i) * 1024), 16, 0, 0);
@@ -367,7 +375,7 @@ sparse_attn_kernel(AttnArgs a) {
 #pragma unroll
     for (int i = 0; i < C::VUPW; ++i) {
       if (C::VUNITS % C::NW == 0 || wave * C::VUPW + i < C::VUNITS) {
-        const char* src = tail ? vbase + min(key0 + v_row(i), klast) * vrow_bytes + v_col(i)
+        const char* src = tail ? vbase + min(key0 + v_row(i), int64_t{klast}) * vrow_bytes + v_col(i)
                                : vb0 + v_lo[i];
         __builtin_amdgcn_global_load_lds(
             src, RCSA_LDS(void, dst + C::KBYTES + (wave * C::VUPW + i) * 1024), 16, 0, 0);
@@ -376,22 +384,22 @@ sparse_attn_kernel(AttnArgs a) {
   };
   // Ring step `it`: step SUB*n + it%SUB of list entry n = list[it / SUB]
   // (-1 = invalid entry), a scalar load.
-  auto block_step = [&](int64_t n, int64_t it) __attribute__((always_inline)) -> int64_t {
-    return (n >= 0 && n < a.n_kblocks) ? n * C::SUB + it % C::SUB : -1;
+  auto block_step = [&](int n, int it) __attribute__((always_inline)) -> int {
+    return (n >= 0 && n < nkb) ? n * C::SUB + it % C::SUB : -1;
   };
-  auto block_of = [&](int64_t it) __attribute__((always_inline)) -> int64_t {
+  auto block_of = [&](int it) __attribute__((always_inline)) -> int {
     return block_step(ld_const(list + it / C::SUB), it);
   };
-  auto fetch_scale = [&](int64_t n) __attribute__((always_inline)) -> float {
+  auto fetch_scale = [&](int n) __attribute__((always_inline)) -> float {
     return INT8 ? ld_const(a.k_scale + bh * a.k_scale_stride + (n < 0 ? 0 : n / C::SUB))
                 : 1.0f;
   };
   // The BNS validity bytes of a step ride along with its copies (BNS/16
   // lanes of wavefront 0, 16 bytes each) into the slot's 256-byte tail;
   // K_valid is 16-byte aligned and readable up to the next 16-byte boundary.
-  auto stage_valid = [&](int64_t n, char* dst) __attribute__((always_inline)) {
+  auto stage_valid = [&](int n, char* dst) __attribute__((always_inline)) {
     if (a.kvalid != nullptr && wave == 0 && lane < BNS / 16) {
-      const int64_t key0 = (n < 0 ? 0 : n) * BNS;
+      const int64_t key0 = static_cast<int64_t>(n < 0 ? 0 : n) * BNS;
       const int64_t chunk = min(key0 + 16 * lane, (klast / 16) * 16);
       const char* src = reinterpret_cast<const char*>(a.kvalid) + chunk;
       __builtin_amdgcn_global_load_lds(src, RCSA_LDS(void, dst + C::BUF), 16, 0, 0);
@@ -400,25 +408,29 @@ sparse_attn_kernel(AttnArgs a) {
   // validity of the wavefront's HK keys of step n from the caller's bits
   // (uniform scalar loads; keys past K_LEN are cleared)
   // (split in two: the raw words, loaded ahead, and the mask of step n)
-  auto mask_words = [&](int64_t n) __attribute__((always_inline)) -> uint2 {
+  auto mask_words = [&](int n) __attribute__((always_inline)) -> uint2 {
     const uint32_t* w = a.kmask + ((n < 0 ? 0 : n) * BNS + kh * C::HK) / 32;
     return make_uint2(ld_const(w), C::HK == 64 ? ld_const(w + 1) : 0u);
   };
-  auto mask_of = [&](int64_t n, uint2 words) __attribute__((always_inline)) -> uint64_t {
+  auto mask_of = [&](int n, uint2 words) __attribute__((always_inline)) -> uint64_t {
     if (n < 0) return 0;
-    const int64_t key0 = n * BNS + kh * C::HK;
+    const int key0 = n * BNS + kh * C::HK;
     uint64_t m = words.x | (static_cast<uint64_t>(words.y) << 32);
-    const int64_t left = a.k_len - key0;
+    const int left = klen - key0;
     if (left < C::HK) m &= left <= 0 ? 0ull : ((1ull << left) - 1);
     return m;
   };
-  auto mask_bits = [&](int64_t n) __attribute__((always_inline)) -> uint64_t {
+  auto mask_bits = [&](int n) __attribute__((always_inline)) -> uint64_t {
     return mask_of(n, mask_words(n));
   };
+  // Validity bits come from the caller when MASK is set; the 3-slot ring is
+  // launched with MASK whenever the caller passes bits, so without MASK it
+  // always takes the bytes (and drops the bit path at compile time).
+  const bool use_bits = MASK || (!kDmaInPv && a.kmask != nullptr);
   // validity of this lane's key in the wavefront's half, from the slot tail
-  auto key_valid = [&](int64_t n, const char* tile) __attribute__((always_inline)) -> bool {
-    const int64_t key = n * BNS + kh * C::HK + lane;
-    if (n < 0 || lane >= C::HK || key >= a.k_len) return false;
+  auto key_valid = [&](int n, const char* tile) __attribute__((always_inline)) -> bool {
+    const int key = n * BNS + kh * C::HK + lane;
+    if (n < 0 || lane >= C::HK || key >= klen) return false;
     return a.kvalid == nullptr || tile[C::BUF + kh * C::HK + lane] != 0;
   };
 
@@ -457,10 +469,9 @@ sparse_attn_kernel(AttnArgs a) {
   // when the caller passes validity bits; `prefetch` issues scalar loads for
   // later blocks once this block's QK MFMAs are issued (scalar loads return
   // out of order, so any LDS wait behind them waits for them too).
-  auto compute = [&](const char* tile, int64_t n, float kscale, uint64_t bits, int64_t n_fill,
+  auto compute = [&](const char* tile, int n, float kscale, uint64_t bits, int n_fill,
                      char* fill, auto&& prefetch) __attribute__((always_inline)) {
-    const uint64_t vmask =
-        (MASK || a.kmask != nullptr) ? bits : __ballot(key_valid(n, tile));
+    const uint64_t vmask = use_bits ? bits : __ballot(key_valid(n, tile));
     const bool all_valid = vmask == (~0ull >> (64 - C::HK));
     // ---- S^T = K Q^T: every K operand read is issued before the MFMAs ----
     AccT s_acc[C::KT];
@@ -588,10 +599,9 @@ sparse_attn_kernel(AttnArgs a) {
   // ---- ring: block j lives in slot j % STAGES; STAGES-1 blocks in flight ----
   // List entries are read one iteration before they are staged (scalar
   // loads whose latency hides behind that iteration's compute).
-  int64_t n_m[3] = {-1, -1, -1};
+  int n_m[3] = {-1, -1, -1};
   float ks_m[3] = {1.0f, 1.0f, 1.0f};
   uint2 mk_m[3] = {};  // raw validity words per slot (caller's bits only)
-  const bool use_bits = MASK || a.kmask != nullptr;
   if constexpr (kDmaInPv) {
     // both prologue steps always copy (step 0 stands in past the list), so
     // every wavefront has exactly 2 * kOps copies in flight
@@ -619,12 +629,12 @@ sparse_attn_kernel(AttnArgs a) {
       }
     }
   }
-  int64_t n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;  // next step to stage
+  int n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;  // next step to stage
   // 3-slot ring: the list entry of the step after n_pre, as loaded
   // (read only when the list is not empty: an empty list may have no entries)
   int32_t pre_raw =
       (kDmaInPv && steps > 0) ? ld_const(list + (STAGES < steps ? STAGES : 0) / C::SUB) : -1;
-  auto iteration = [&](auto slot_c, int64_t j) __attribute__((always_inline)) {
+  auto iteration = [&](auto slot_c, int j) __attribute__((always_inline)) {
     constexpr int J = decltype(slot_c)::value;
     constexpr int F = (J + STAGES - 1) % STAGES;  // slot of block j + STAGES - 1
     char* const tile = J == 0 ? s_0 : J == 1 ? s_1 : s_2;
@@ -650,10 +660,10 @@ sparse_attn_kernel(AttnArgs a) {
       // Loaded values are only stored here (their first use is a later
       // block's), so no wait lands before this block's softmax.
       constexpr int N1 = (J + 1) % STAGES;  // slot of block j + 1
-      const int64_t nf = n_pre;
+      const int nf = n_pre;
       n_m[F] = nf;
       n_pre = j + STAGES < steps ? block_step(pre_raw, j + STAGES) : -1;
-      const int64_t nxt = j + STAGES + 1 < steps ? j + STAGES + 1 : 0;  // in-bounds entry
+      const int nxt = j + STAGES + 1 < steps ? j + STAGES + 1 : 0;  // in-bounds entry
       compute(tile, n_m[J], ks_m[J], use_bits ? mask_of(n_m[J], mk_m[J]) : 0ull, nf, fill,
               [&]() __attribute__((always_inline)) {
                 ks_m[F] = fetch_scale(nf);
@@ -672,7 +682,7 @@ sparse_attn_kernel(AttnArgs a) {
               []() __attribute__((always_inline)) {});
     }
   };
-  for (int64_t j = 0; j < steps; j += STAGES) {
+  for (int j = 0; j < steps; j += STAGES) {
     iteration(std::integral_constant<int, 0>{}, j);
     if (j + 1 >= steps) break;
     iteration(std::integral_constant<int, 1>{}, j + 1);
@@ -934,7 +944,9 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   a.n_bh = B * H;
   a.n_items = B * H * a.n_qblocks;
   // the kernel decodes work items and list shares in 32-bit arithmetic
-  if (a.n_items >= (int64_t{1} << 31) || max_k >= (int64_t{1} << 24)) return RCSA_ERR_SHAPE;
+  if (a.n_items >= (int64_t{1} << 31) || max_k >= (int64_t{1} << 24) ||
+      K_LEN >= (int64_t{1} << 31))
+    return RCSA_ERR_SHAPE;
   a.xcd_items = (a.n_items + kNumXcd - 1) / kNumXcd;
   a.xcd_direct = a.xcd_items;
   a.n_split = 1;
