@@ -176,6 +176,21 @@ struct AttnCfg {
   static_assert(BNS <= 256, "validity bytes of one step fit the slot tail");
 };
 
+// Direct-to-LDS copy of 16 (4) bytes per lane through a buffer resource over
+// [base, base + bytes): a lane whose bytes do not fit below `bytes` reads
+// zeros and touches no memory.
+// (The LDS destination is passed as a generic pointer: an LDS-typed
+// parameter makes the host pass of the kernel templates drop their stubs.)
+constexpr int kRsrcWord3 = 0x00020000;  // raw untyped buffer, 32-bit data format
+__device__ __forceinline__ void buffer_copy16(char* base, int bytes, uint32_t voff, char* dst) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kRsrcWord3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RCSA_LDS(void, dst), 16, voff, 0, 0, 0);
+}
+__device__ __forceinline__ void buffer_copy4(char* base, int bytes, uint32_t voff, char* dst) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kRsrcWord3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RCSA_LDS(void, dst), 4, voff, 0, 0, 0);
+}
+
 // Waves per SIMD the register budget is sized for.  A ring of BNS < BN keys
 // fits two workgroups in one compute unit's LDS, so exactly two waves of
 // each SIMD's share must fit; otherwise the compiler's default range applies
@@ -308,55 +323,41 @@ sparse_attn_kernel(AttnArgs a) {
   // slot.  Rows past k_len re-read the last row (those keys are masked).
   // (Named source pointers: an inline pointer expression as this builtin's
   // source argument makes the host pass drop the kernel stub.)
-  // Branch-free variant: every lane offset is min(row, rows_left - 1) *
-  // row_bytes + chunk (24-bit multiply; row strides stay below 16 MiB), so
-  // the copies sit in the caller's basic block between its MFMAs.
-  int k_r[C::KUPW], k_c[C::KUPW], v_r[C::VUPW], v_c[C::VUPW];
-#pragma unroll
-  for (int i = 0; i < C::KUPW; ++i) { k_r[i] = k_row(i); k_c[i] = k_col(i); }
-#pragma unroll
-  for (int i = 0; i < C::VUPW; ++i) { v_r[i] = v_row(i); v_c[i] = v_col(i); }
+  // Branch-free variant for the 3-slot ring: the copies of a step go through
+  // buffer resources that end at the step's last valid row, so each lane
+  // keeps its loop-invariant offset and rows past K_LEN land as zeros (those
+  // keys are masked); the copies then sit in the caller's basic block
+  // between its MFMAs.
   const uint32_t krb = static_cast<uint32_t>(krow_bytes), vrb = static_cast<uint32_t>(vrow_bytes);
   auto stage_flat = [&](int n, char* dst) __attribute__((always_inline)) {
     int key0 = (n < 0 ? 0 : n) * BNS;
     key0 = key0 > klast ? klast : key0;
     const int left = klen - key0;  // >= 1
-    const uint32_t lim = static_cast<uint32_t>(left < BNS ? left - 1 : BNS - 1);
-    const char* kb0 = kbase + static_cast<int64_t>(key0) * krow_bytes;
-    const char* vb0 = vbase + static_cast<int64_t>(key0) * vrow_bytes;
+    const int rows = left < BNS ? left : BNS;
+    char* const kb0 = const_cast<char*>(kbase) + static_cast<int64_t>(key0) * krow_bytes;
+    char* const vb0 = const_cast<char*>(vbase) + static_cast<int64_t>(key0) * vrow_bytes;
+    // rows * row bytes < 2^31: row strides stay below 16 MiB
+    const int knum = rows * static_cast<int>(krb), vnum = rows * static_cast<int>(vrb);
 #pragma unroll
-    for (int i = 0; i < C::KUPW; ++i) {
-      // uniform base + zero-extended 32-bit lane offset: the SGPR-base form
-      const uint32_t off = __umul24(min(static_cast<uint32_t>(k_r[i]), lim), krb) +
-                           static_cast<uint32_t>(k_c[i]);
-      const char* src = kb0 + off;
-      __builtin_amdgcn_global_load_lds(
-          src, RCSA_LDS(void, dst + (wave * C::KUPW + i) * 1024), 16, 0, 0);
-    }
+    for (int i = 0; i < C::KUPW; ++i)
+      buffer_copy16(kb0, knum, k_lo[i], dst + (wave * C::KUPW + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < C::VUPW; ++i) {
-      const uint32_t off = __umul24(min(static_cast<uint32_t>(v_r[i]), lim), vrb) +
-                           static_cast<uint32_t>(v_c[i]);
-      const char* src = vb0 + off;
-      __builtin_amdgcn_global_load_lds(
-          src, RCSA_LDS(void, dst + C::KBYTES + (wave * C::VUPW + i) * 1024), 16, 0, 0);
-    }
+    for (int i = 0; i < C::VUPW; ++i)
+      buffer_copy16(vb0, vnum, v_lo[i], dst + C::KBYTES + (wave * C::VUPW + i) * 1024);
   };
   // validity bytes of step n, 4 per lane from every wavefront (lanes 32-63
-  // repeat lanes 0-31 into the tail's unused half); offsets past the
-  // readable range are clamped and stand for keys past K_LEN
-  const uint8_t* kvb = a.kvalid != nullptr ? a.kvalid : kAllValid;
-  const int64_t kv_step = a.kvalid != nullptr ? 1 : 0;
-  const int64_t kv_last = a.kvalid != nullptr ? (a.k_len + 15) / 16 * 16 - 4 : 124;
+  // repeat lanes 0-31 into the tail's unused half), through a buffer that
+  // ends at the dword holding the last key (K_valid is readable up to its
+  // next 16-byte boundary; bytes of keys past K_LEN are masked anyway)
   auto stage_valid_flat = [&](int n, char* dst) __attribute__((always_inline)) {
     static_assert(BNS <= 128, "validity bytes of a step: 32 lanes x 4");
-    int64_t key0 = static_cast<int64_t>(n < 0 ? 0 : n) * BNS;
-    key0 = key0 > klast ? klast / 16 * 16 : key0;
-    const int64_t vk0 = key0 * kv_step;
-    const uint32_t vlim = static_cast<uint32_t>(kv_last - vk0 < 124 ? kv_last - vk0 : 124);
-    const char* vsrc = reinterpret_cast<const char*>(kvb) + vk0 +
-                       min(static_cast<uint32_t>(4 * (lane & 31)), vlim);
-    __builtin_amdgcn_global_load_lds(vsrc, RCSA_LDS(void, dst + C::BUF), 4, 0, 0);
+    const int key0 = (n < 0 ? 0 : n) * BNS;  // a listed block starts below K_LEN
+    const bool has = a.kvalid != nullptr;
+    char* const vb = has ? reinterpret_cast<char*>(const_cast<uint8_t*>(a.kvalid)) + key0
+                         : reinterpret_cast<char*>(kAllValid);
+    const int left = has ? klen - key0 : BNS;
+    const int vnum = ((left + 3) & ~3) < BNS ? ((left + 3) & ~3) : BNS;
+    buffer_copy4(vb, vnum, 4u * (lane & 31), dst + C::BUF);
   };
   auto stage = [&](int n, char* dst) __attribute__((always_inline)) {
     const int64_t key0 = static_cast<int64_t>(n < 0 ? 0 : n) * BNS;
