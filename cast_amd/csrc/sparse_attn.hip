@@ -638,6 +638,9 @@ sparse_attn_kernel(AttnArgs a) {
   auto iteration = [&](auto slot_c, int j) __attribute__((always_inline)) {
     constexpr int J = decltype(slot_c)::value;
     constexpr int F = (J + STAGES - 1) % STAGES;  // slot of block j + STAGES - 1
+    // keep the int8 bias tile in VGPRs (otherwise it lives in SGPRs and is
+    // copied into VGPRs for every block's first QK MFMA)
+    if constexpr (INT8) asm volatile("" : "+v"(c_init));
     char* const tile = J == 0 ? s_0 : J == 1 ? s_1 : s_2;
     char* const fill = F == 0 ? s_0 : F == 1 ? s_1 : s_2;
     // block j's copies are the oldest in flight; the STAGES-2 younger
