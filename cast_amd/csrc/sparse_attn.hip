@@ -334,8 +334,11 @@ sparse_attn_kernel(AttnArgs a) {
     key0 = key0 > klast ? klast : key0;
     const int left = klen - key0;  // >= 1
     const int rows = left < BNS ? left : BNS;
-    char* const kb0 = const_cast<char*>(kbase) + static_cast<int64_t>(key0) * krow_bytes;
-    char* const vb0 = const_cast<char*>(vbase) + static_cast<int64_t>(key0) * vrow_bytes;
+    // (key0 and the row strides are below 2^31: 32 x 32 -> 64-bit products)
+    char* const kb0 = const_cast<char*>(kbase) +
+                      static_cast<uint64_t>(static_cast<uint32_t>(key0)) * krb;
+    char* const vb0 = const_cast<char*>(vbase) +
+                      static_cast<uint64_t>(static_cast<uint32_t>(key0)) * vrb;
     // rows * row bytes < 2^31: row strides stay below 16 MiB
     const int knum = rows * static_cast<int>(krb), vnum = rows * static_cast<int>(vrb);
 #pragma unroll
@@ -386,7 +389,8 @@ sparse_attn_kernel(AttnArgs a) {
   // Ring step `it`: step SUB*n + it%SUB of list entry n = list[it / SUB]
   // (-1 = invalid entry), a scalar load.
   auto block_step = [&](int n, int it) __attribute__((always_inline)) -> int {
-    return (n >= 0 && n < nkb) ? n * C::SUB + it % C::SUB : -1;
+    // one unsigned compare rejects both -1 padding and entries past the keys
+    return static_cast<uint32_t>(n) < static_cast<uint32_t>(nkb) ? n * C::SUB + it % C::SUB : -1;
   };
   auto block_of = [&](int it) __attribute__((always_inline)) -> int {
     return block_step(ld_const(list + it / C::SUB), it);
@@ -413,13 +417,16 @@ sparse_attn_kernel(AttnArgs a) {
     const uint32_t* w = a.kmask + ((n < 0 ? 0 : n) * BNS + kh * C::HK) / 32;
     return make_uint2(ld_const(w), C::HK == 64 ? ld_const(w + 1) : 0u);
   };
+  // Only the step holding K_LEN can have keys past it: its keep mask for this
+  // wavefront's half is computed once.
+  const int tail_step = klen % BNS != 0 ? klen / BNS : -1;
+  const uint64_t tail_keep = [&]() -> uint64_t {
+    const int left = klen - (klen / BNS * BNS + kh * C::HK);
+    return left >= C::HK ? ~0ull : (left <= 0 ? 0ull : ((1ull << left) - 1));
+  }();
   auto mask_of = [&](int n, uint2 words) __attribute__((always_inline)) -> uint64_t {
-    if (n < 0) return 0;
-    const int key0 = n * BNS + kh * C::HK;
-    uint64_t m = words.x | (static_cast<uint64_t>(words.y) << 32);
-    const int left = klen - key0;
-    if (left < C::HK) m &= left <= 0 ? 0ull : ((1ull << left) - 1);
-    return m;
+    const uint64_t m = words.x | (static_cast<uint64_t>(words.y) << 32);
+    return n < 0 ? 0ull : (n == tail_step ? m & tail_keep : m);
   };
   auto mask_bits = [&](int n) __attribute__((always_inline)) -> uint64_t {
     return mask_of(n, mask_words(n));
