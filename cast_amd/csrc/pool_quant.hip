@@ -100,8 +100,7 @@ struct Raw8<float> {
 // are in flight, and the per-channel partials are reduced across the row
 // groups of a wavefront by shuffles before one small LDS pass.
 template <typename T, int D, int BS, bool QUANT, bool STATS>
-__global__ void __launch_bounds__(kPoolThreads)
-pool_kernel(PoolArgs a) {
+__device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
   constexpr int CPR = D / 8;                 // 16-byte chunks per token row
   constexpr int RG = kPoolThreads / CPR;     // row groups
   constexpr int ROWS = BS / RG;              // rows per thread
@@ -114,8 +113,8 @@ pool_kernel(PoolArgs a) {
   __shared__ uint8_t s_valid[BS];
   __shared__ float s_red[4];
 
-  const int64_t blk = blockIdx.x % a.n_blocks;
-  const int64_t bh = blockIdx.x / a.n_blocks;
+  const int64_t blk = tile % a.n_blocks;
+  const int64_t bh = tile / a.n_blocks;
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
   const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
                blk * BS * a.stride_t;
@@ -219,6 +218,23 @@ pool_kernel(PoolArgs a) {
       *reinterpret_cast<uint2*>(out + r * D + c * 8) = make_uint2(lo, hi);
     }
   }
+}
+
+template <typename T, int D, int BS, bool QUANT, bool STATS>
+__global__ void __launch_bounds__(kPoolThreads)
+pool_kernel(PoolArgs a) {
+  pool_tile<T, D, BS, QUANT, STATS>(a, blockIdx.x);
+}
+
+// Query pooling (with its int8 quantiser) and key pooling (with the key
+// statistics) in one launch: the first q_tiles workgroups take query tiles,
+// the rest key tiles.  The short, latency-bound query pass then runs inside
+// the HBM-bound key pass instead of before it.
+template <typename T, int D, int BS>
+__global__ void __launch_bounds__(kPoolThreads)
+pool_qk_kernel(PoolArgs q, PoolArgs k, int64_t q_tiles) {
+  if (blockIdx.x < q_tiles) pool_tile<T, D, BS, true, false>(q, blockIdx.x);
+  else pool_tile<T, D, BS, false, true>(k, blockIdx.x - q_tiles);
 }
 
 // Cosine scores: one workgroup per (bh, 16 query blocks, 64 key blocks).
@@ -470,6 +486,43 @@ extern "C" int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_
     if (stats) launch_pool<float, false, true>(a, nbh, block_size, head_dim, stream);
     else launch_pool<float, false, false>(a, nbh, block_size, head_dim, stream);
   }
+  return launch_status();
+}
+
+extern "C" int rcsa_pool_query_key(
+    const void* q, const void* k, int dtype, int64_t batch, int64_t n_heads,
+    int64_t n_qblocks, int64_t n_kblocks, int64_t block_size, int64_t head_dim,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
+    int64_t k_stride_h, int64_t k_stride_t, const uint8_t* q_valid, const uint8_t* k_valid,
+    float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum, float* kmin,
+    float* kmax, uint32_t* block_mask, hipStream_t stream) {
+  if (!q || !k || !qhat || !q_i8 || !q_scale || !khat || !ksum || !kmin || !kmax)
+    return RCSA_ERR_NULL;
+  int st = check_pool_shape(dtype, batch, n_heads, n_qblocks, block_size, head_dim,
+                            q_stride_b, q_stride_h, q_stride_t);
+  if (st) return st;
+  st = check_pool_shape(dtype, batch, n_heads, n_kblocks, block_size, head_dim, k_stride_b,
+                        k_stride_h, k_stride_t);
+  if (st) return st;
+  if (!aligned16(q) || !aligned16(k) || (reinterpret_cast<uintptr_t>(q_i8) & 7u))
+    return RCSA_ERR_ALIGN;
+  if (block_mask && (reinterpret_cast<uintptr_t>(block_mask) & 7u)) return RCSA_ERR_ALIGN;
+  const PoolArgs qa{q, n_heads, n_qblocks, q_stride_b, q_stride_h, q_stride_t, q_valid, qhat,
+                    nullptr, nullptr, nullptr, q_i8, q_scale, nullptr};
+  const PoolArgs ka{k, n_heads, n_kblocks, k_stride_b, k_stride_h, k_stride_t, k_valid, khat,
+                    ksum, kmin, kmax, nullptr, nullptr, block_mask};
+  const int64_t nbh = batch * n_heads;
+  const int64_t q_tiles = nbh * n_qblocks;
+  const dim3 grid(static_cast<unsigned>(q_tiles + nbh * n_kblocks)), block(kPoolThreads);
+#define RCSA_PQK(T_, D_, BS_) pool_qk_kernel<T_, D_, BS_><<<grid, block, 0, stream>>>(qa, ka, q_tiles)
+#define RCSA_PQK_T(T_)                                               \
+  if (head_dim == 128 && block_size == 128) RCSA_PQK(T_, 128, 128);  \
+  else if (head_dim == 128) RCSA_PQK(T_, 128, 64);                   \
+  else if (block_size == 128) RCSA_PQK(T_, 64, 128);                 \
+  else RCSA_PQK(T_, 64, 64);
+  if (dtype == RCSA_BF16) { RCSA_PQK_T(u16) } else { RCSA_PQK_T(float) }
+#undef RCSA_PQK_T
+#undef RCSA_PQK
   return launch_status();
 }
 

@@ -127,6 +127,40 @@ def pool_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
     return (khat, ksum, kmin, kmax, mask) if block_mask else (khat, ksum, kmin, kmax)
 
 
+def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Tensor,
+                   k_valid: Optional[torch.Tensor], block_size: int):
+    """``pool_query(q, q_valid, quantize=True)`` and ``pool_key(k, k_valid, stats=True,
+    block_mask=True)`` in one launch (no reference counterpart: the int8 layer call's
+    pooling pass).  Returns ``(qhat, q_i8, q_scale, khat, ksum, kmin, kmax, block_mask)``,
+    bit for bit the two calls' outputs.
+    """
+    fn = "pool_query_key"
+    _require_cuda(fn, q, k)
+    code = _dtype_code(q, fn)
+    if _dtype_code(k, fn) != code:
+        raise TypeError(f"{fn}: q and k must share a dtype")
+    B, H, Lq, D, NQ = _bhld(q, block_size, fn)
+    Bk, Hk, Lk, Dk, NK = _bhld(k, block_size, fn)
+    if (Bk, Hk, Dk) != (B, H, D):
+        raise ValueError(f"{fn}: q {tuple(q.shape)} and k {tuple(k.shape)} differ in B, H or D")
+    qv = _valid_u8(q_valid, Lq, q.device, fn)
+    kv = _valid_u8(k_valid, Lk, k.device, fn)
+    f32 = dict(device=q.device, dtype=torch.float32)
+    qhat = torch.empty(B * H, NQ, D, **f32)
+    q_i8 = torch.empty(B, H, Lq, D, device=q.device, dtype=torch.int8)
+    q_scale = torch.empty(B * H, NQ, **f32)
+    khat, ksum, kmin, kmax = (torch.empty(B * H, NK, D, **f32) for _ in range(4))
+    mask = torch.empty(NK, block_size // 32, device=k.device, dtype=torch.int32)
+    st = _lib.load().rcsa_pool_query_key(
+        q.data_ptr(), k.data_ptr(), code, B, H, NQ, NK, block_size, D,
+        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(qv), _ptr(kv), qhat.data_ptr(), q_i8.data_ptr(), q_scale.data_ptr(),
+        khat.data_ptr(), ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), mask.data_ptr(),
+        _stream())
+    check(st, fn)
+    return qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask
+
+
 def block_scores(qhat: torch.Tensor, khat: torch.Tensor) -> torch.Tensor:
     """``score[bh] = qhat[bh] @ khat[bh]^T`` (P/matrix_curvature_phase_frame_weave.py:5701)."""
     fn = "block_scores"

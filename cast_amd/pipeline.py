@@ -82,11 +82,11 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         with torch.cuda.stream(side):
             return fn()
 
-    qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs, quantize=int8)
-    if int8:  # the validity bits come with the pooling pass
-        khat, ksum, kmin, kmax, k_mask = ops.pool_key(k, k_valid, bs, stats=True,
-                                                      block_mask=True)
+    if int8:  # one launch pools Q (+ int8) and K (+ stats and validity bits)
+        qhat, q_i8, q_scale, khat, ksum, kmin, kmax, k_mask = ops.pool_query_key(
+            q, q_valid, k, k_valid, bs)
     else:
+        qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs)
         khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs)
         k_mask = None
     if side is not None:

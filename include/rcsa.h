@@ -94,6 +94,23 @@ int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
                   float* kmax, uint32_t* block_mask, hipStream_t stream);
 
 /*
+ * rcsa_pool_query (with q_i8 / q_scale) and rcsa_pool_key (with ksum / kmin /
+ * kmax and, if non-NULL, block_mask) in one launch; the outputs are those of
+ * the two calls bit for bit.  No reference counterpart: the int8 layer call's
+ * pooling pass, so the short query pass runs inside the key pass instead of
+ * before it.  Q and K share dtype, batch, heads, block_size and head_dim; each
+ * has its own block count, strides and validity.
+ */
+int rcsa_pool_query_key(const void* q, const void* k, int dtype, int64_t batch,
+                        int64_t n_heads, int64_t n_qblocks, int64_t n_kblocks,
+                        int64_t block_size, int64_t head_dim, int64_t q_stride_b,
+                        int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
+                        int64_t k_stride_h, int64_t k_stride_t, const uint8_t* q_valid,
+                        const uint8_t* k_valid, float* qhat, int8_t* q_i8, float* q_scale,
+                        float* khat, float* ksum, float* kmin, float* kmax,
+                        uint32_t* block_mask, hipStream_t stream);
+
+/*
  * Cosine block scores score[bh, i, j] = <qhat[bh, i], khat[bh, j]>.
  * Replaces torch.matmul(q_content, k_content.transpose(-2, -1)) at
  * P/matrix_curvature_phase_frame_weave.py:5701 and

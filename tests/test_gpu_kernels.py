@@ -78,6 +78,23 @@ def test_pool_key_stats_and_quantize(dev, D, bs):
     assert torch.equal(k8.cpu(), ref8)
 
 
+@pytest.mark.parametrize("D,bs,dtype", [(128, 128, torch.bfloat16), (64, 64, torch.float32),
+                                        (128, 64, torch.bfloat16)])
+def test_pool_query_key_fused(dev, D, bs, dtype):
+    """The fused pooling launch equals the two separate calls bit for bit."""
+    from cast_amd import ops
+    q, k, _, qv, kv = _case(4, D=D, bs=bs, dtype=dtype, q_valid_tail=bs // 2,
+                            k_valid_tail=bs + 17)
+    q, k, qv, kv = q.to(dev), k.to(dev), qv.to(dev), kv.to(dev)
+    got = ops.pool_query_key(q, qv, k, kv, bs)
+    ref = ops.pool_query(q, qv, bs, quantize=True) + ops.pool_key(k, kv, bs, stats=True,
+                                                                    block_mask=True)
+    torch.cuda.synchronize()
+    names = ("qhat", "q_i8", "q_scale", "khat", "ksum", "kmin", "kmax", "block_mask")
+    for name, a, b in zip(names, got, ref):
+        assert torch.equal(a, b), name
+
+
 def test_block_scores(dev):
     from cast_amd import ops
     g = torch.Generator().manual_seed(3)
