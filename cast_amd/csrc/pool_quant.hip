@@ -317,6 +317,16 @@ kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
   const float* src = ksum + bh * n_blocks * D + c0 + c;
   float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
   int64_t b = bl;
+  // sixteen loads in flight per pass; the adds keep the four chains' order
+  for (; b + 15 * BL < n_blocks; b += 16 * BL) {
+    float v[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) v[k] = src[(b + k * BL) * D];
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] += v[4 * g + u];
+  }
   for (; b + 3 * BL < n_blocks; b += 4 * BL) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc[u] += src[(b + u * BL) * D];
@@ -329,7 +339,17 @@ kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
   } else if ((reinterpret_cast<uintptr_t>(valid) & 15u) == 0) {
     const int64_t n16 = n_tokens / 16;
     const uint4* v4 = reinterpret_cast<const uint4*>(valid);
-    for (int64_t i = t; i < n16; i += 256) {
+    int64_t i0 = t;
+    for (; i0 + 3 * 256 < n16; i0 += 4 * 256) {  // four 16-byte loads in flight
+      uint4 w[4];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) w[k] = v4[i0 + k * 256];
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        cnt += nonzero_bytes(w[k].x) + nonzero_bytes(w[k].y) + nonzero_bytes(w[k].z) +
+               nonzero_bytes(w[k].w);
+    }
+    for (int64_t i = i0; i < n16; i += 256) {
       const uint4 w = v4[i];
       cnt += nonzero_bytes(w.x) + nonzero_bytes(w.y) + nonzero_bytes(w.z) + nonzero_bytes(w.w);
     }
