@@ -121,6 +121,48 @@ def cpu_baseline(seed: int, heads: int) -> dict:
                       f"scaled x{w.q.shape[1] / heads:g}"}
 
 
+def compact_layout_call(seed: int, iters: int) -> dict:
+    """The int8 layer call on token-major Q/K/V of the Matrix latent grid (22 x 40
+    tokens per frame, (4, 4, 8) tiles with 64-token bottom tiles; 4 query frames,
+    40 memory + 4 current key frames; 24 heads, D 128; history budget 25% + the
+    current blocks): packing fused into the kernels (slot maps) against
+    pack_tokens -> packed layer call -> unpack_tokens."""
+    import torch
+    from cast_amd import layout, ops
+    from cast_amd.pipeline import rcsa_attention
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    hw, shape, H, D = (22, 40), (4, 4, 8), 24, 128
+    lay_q = layout.compact_layout(range(4), 0, *hw, shape, dev)
+    lay_k = layout.compact_layout(range(44), 40, *hw, shape, dev)
+    lq, lk = 4 * 880, 44 * 880
+    q, k, v = (torch.randn(1, n, H, D, device=dev, generator=g).div_(D ** 0.5)
+               .to(torch.bfloat16) for n in (lq, lk, lk))
+    nq, nk = lay_q.n_blocks, lay_k.n_blocks
+    forced = torch.zeros(nq, nk, dtype=torch.bool)
+    forced[:, nk - 30:] = True
+    k_sel = round(0.25 * (nk - 30)) + 30
+
+    def fused():
+        return rcsa_attention(q, k, v, None, None, block_size=128, k_select=k_sel,
+                              forced=forced, int8=True, max_k=k_sel,
+                              q_slot_token=lay_q.slot_token, k_slot_token=lay_k.slot_token).out
+
+    def unfused():
+        r = rcsa_attention(ops.pack_tokens(q, lay_q.slot_token), ops.pack_tokens(k, lay_k.slot_token),
+                           ops.pack_tokens(v, lay_k.slot_token), lay_q.slot_valid,
+                           lay_k.slot_valid, block_size=128, k_select=k_sel, forced=forced,
+                           int8=True, max_k=k_sel)
+        return ops.unpack_tokens(r.out, lay_q.token_to_packed)
+
+    same = bool(torch.equal(fused(), unfused()))
+    _prewarm(fused, 40.0)
+    f_ms = _events_time(fused, iters)
+    u_ms = _events_time(unfused, iters)
+    return {"fused_ms": f_ms, "pack_unpack_ms": u_ms, "outputs_equal": same,
+            "q_blocks": nq, "k_blocks": nk, "k_select": k_sel}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -325,6 +367,7 @@ def main() -> int:
         extras["step_sweep_30_layers"] = {"ms_per_step": step_ms,
                                           "effective_TOPS": sweep_ops / step_ms / 1e9}
         del layers
+        extras["compact_layout_call"] = compact_layout_call(args.seed, iters)
 
     line["extras"] = extras
     if not args.no_cpu_baseline:

@@ -25,19 +25,19 @@ SIGNATURES: dict[str, list] = {
     "rcsa_pool_query": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P],
     "rcsa_pool_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "rcsa_pool_query_key": [_P, _P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
-                            _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+                            _P, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "rcsa_block_scores": [_P, _P, _I, _I, _I, _I, _P, _P],
     "rcsa_select_topk": [_P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _P, _I, _P, c_int, _P],
-    "rcsa_quantize_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P,
-                          _P, _P, _P],
+    "rcsa_quantize_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P,
+                          _P, _P, _P, _P],
     "rcsa_sparse_attn_bf16": [_P, _P, _P, _P, c_float, _P, _P, _P, _P] + [_I] * 18
                              + [_I] * 8 + [_P],
     "rcsa_sparse_attn_int8": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P, _P]
-                             + [_I] * 18 + [_I] * 8 + [_P],
+                             + [_I] * 18 + [_I] * 8 + [_P, _I, _P],
     "rcsa_sparse_attn_bf16_split": [_P, _P, _P, _P, c_float, _P, _P, _P, _P] + [_I] * 18
                                    + [_I] * 8 + [_I, _P, _I, _P],
     "rcsa_sparse_attn_int8_split": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P, _P]
-                                   + [_I] * 18 + [_I] * 8 + [_I, _P, _I, _P],
+                                   + [_I] * 18 + [_I] * 8 + [_I, _P, _I, _P, _I, _P],
     "rcsa_attn_workspace_bytes": [_I, _I, _I, _I, _I],
     "rcsa_attn_split_plan": [_I, _I, _I, _I, _I, ctypes.POINTER(c_int64)],
     "rcsa_pack_tokens": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],

@@ -23,7 +23,33 @@ struct PoolArgs {
   int8_t* x_i8;     // query quantiser output (pool_query only)
   float* x_scale;   // query scales (pool_query only)
   uint32_t* mask;   // per-block validity bits (pool_key only, may be NULL)
+  // Gather map (MAP kernels only): packed slot s = blk * BS + r reads token
+  // slot_tok[s] of x's token axis (stride_t); -1 or a token >= src_len is an
+  // empty slot (invalid, never read).
+  const int32_t* slot_tok;
+  int64_t src_len;
 };
+
+// Source row of packed row r of block blk: the row itself, or through the
+// gather map (an empty slot reads token 0, which its validity then drops).
+template <bool MAP, int BS>
+__device__ __forceinline__ int64_t src_row(const PoolArgs& a, int64_t blk, int r) {
+  if constexpr (!MAP) {
+    return blk * BS + r;
+  } else {
+    const int32_t tk = a.slot_tok[blk * BS + r];
+    return (tk < 0 || tk >= a.src_len) ? 0 : tk;
+  }
+}
+template <bool MAP, int BS>
+__device__ __forceinline__ bool slot_valid(const PoolArgs& a, int64_t blk, int r) {
+  bool v = a.valid == nullptr || a.valid[blk * BS + r] != 0;
+  if constexpr (MAP) {
+    const int32_t tk = a.slot_tok[blk * BS + r];
+    v = v && tk >= 0 && tk < a.src_len;
+  }
+  return v;
+}
 
 // Block-wide helpers (kPoolThreads = 4 waves).
 __device__ __forceinline__ float block_sum(float v, float* red) {
@@ -99,7 +125,7 @@ struct Raw8<float> {
 // its row loads first; the block's validity bytes go through LDS while they
 // are in flight, and the per-channel partials are reduced across the row
 // groups of a wavefront by shuffles before one small LDS pass.
-template <typename T, int D, int BS, bool QUANT, bool STATS>
+template <typename T, int D, int BS, bool QUANT, bool STATS, bool MAP>
 __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
   constexpr int CPR = D / 8;                 // 16-byte chunks per token row
   constexpr int RG = kPoolThreads / CPR;     // row groups
@@ -116,18 +142,18 @@ __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
   const int64_t blk = tile % a.n_blocks;
   const int64_t bh = tile / a.n_blocks;
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
-  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
-               blk * BS * a.stride_t;
+  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h;
   const int t = threadIdx.x;
   const int c = t % CPR, g = t / CPR;
   const int lane = t % kWave, wave = t / kWave;
 
   Raw8<T> raw[ROWS];
 #pragma unroll
-  for (int i = 0; i < ROWS; ++i) raw[i].load(x + (g + RG * i) * a.stride_t + c * 8);
+  for (int i = 0; i < ROWS; ++i)
+    raw[i].load(x + src_row<MAP, BS>(a, blk, g + RG * i) * a.stride_t + c * 8);
   bool tv = false;
   if (t < BS) {
-    tv = a.valid == nullptr || a.valid[blk * BS + t] != 0;
+    tv = slot_valid<MAP, BS>(a, blk, t);
     s_valid[t] = tv;
   }
   // validity bits of the block (every head shares them: head 0 writes)
@@ -223,18 +249,18 @@ __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
 template <typename T, int D, int BS, bool QUANT, bool STATS>
 __global__ void __launch_bounds__(kPoolThreads)
 pool_kernel(PoolArgs a) {
-  pool_tile<T, D, BS, QUANT, STATS>(a, blockIdx.x);
+  pool_tile<T, D, BS, QUANT, STATS, false>(a, blockIdx.x);
 }
 
 // Query pooling (with its int8 quantiser) and key pooling (with the key
 // statistics) in one launch: the first q_tiles workgroups take query tiles,
 // the rest key tiles.  The short, latency-bound query pass then runs inside
 // the HBM-bound key pass instead of before it.
-template <typename T, int D, int BS>
+template <typename T, int D, int BS, bool MAP>
 __global__ void __launch_bounds__(kPoolThreads)
 pool_qk_kernel(PoolArgs q, PoolArgs k, int64_t q_tiles) {
-  if (blockIdx.x < q_tiles) pool_tile<T, D, BS, true, false>(q, blockIdx.x);
-  else pool_tile<T, D, BS, false, true>(k, blockIdx.x - q_tiles);
+  if (blockIdx.x < q_tiles) pool_tile<T, D, BS, true, false, MAP>(q, blockIdx.x);
+  else pool_tile<T, D, BS, false, true, MAP>(k, blockIdx.x - q_tiles);
 }
 
 // Cosine scores: one workgroup per (bh, 16 query blocks, 64 key blocks).
@@ -305,8 +331,8 @@ __device__ __forceinline__ int nonzero_bytes(uint32_t w) {
 // count is taken with 16-byte loads.
 template <int D>
 __global__ void __launch_bounds__(256)
-kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
-             int64_t n_tokens, float* kmean) {
+kmean_kernel(const float* ksum, const uint8_t* valid, const int32_t* slot_tok,
+             int64_t src_len, int64_t n_blocks, int64_t n_tokens, float* kmean) {
   constexpr int CG = 16;          // channels per workgroup
   constexpr int BL = 256 / CG;    // block lanes
   __shared__ float part[BL][CG + 1];
@@ -334,7 +360,12 @@ kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
   for (; b < n_blocks; b += BL) acc[0] += src[b * D];
   part[bl][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   int cnt = 0;
-  if (valid == nullptr) {
+  if (slot_tok != nullptr) {  // gathered keys: a slot counts when it holds a token
+    for (int64_t i = t; i < n_tokens; i += 256) {
+      const int32_t tk = slot_tok[i];
+      cnt += tk >= 0 && tk < src_len && (valid == nullptr || valid[i] != 0);
+    }
+  } else if (valid == nullptr) {
     cnt = t == 0 ? static_cast<int>(n_tokens) : 0;
   } else if ((reinterpret_cast<uintptr_t>(valid) & 15u) == 0) {
     const int64_t n16 = n_tokens / 16;
@@ -369,7 +400,7 @@ kmean_kernel(const float* ksum, const uint8_t* valid, int64_t n_blocks,
 // Smoothed per-block key quantiser: one workgroup per (bh, block).  The tile
 // loads are issued first; the scale (from the block's min/max and the head
 // mean) is computed while they are in flight.
-template <typename T, int D, int BS>
+template <typename T, int D, int BS, bool MAP>
 __global__ void __launch_bounds__(kPoolThreads)
 quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
   constexpr int CPR = D / 8;
@@ -383,14 +414,14 @@ quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
   const int t = threadIdx.x;
   const int c = t % CPR, g = t / CPR;
-  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
-               blk * BS * a.stride_t;
+  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h;
   Raw8<T> raw[ROWS];
 #pragma unroll
-  for (int i = 0; i < ROWS; ++i) raw[i].load(x + (g + RG * i) * a.stride_t + c * 8);
+  for (int i = 0; i < ROWS; ++i)
+    raw[i].load(x + src_row<MAP, BS>(a, blk, g + RG * i) * a.stride_t + c * 8);
   bool tv = false;
   if (t < BS) {
-    tv = a.valid == nullptr || a.valid[blk * BS + t] != 0;
+    tv = slot_valid<MAP, BS>(a, blk, t);
     s_valid[t] = tv;
   }
   float dev = 0.0f;
@@ -470,7 +501,7 @@ extern "C" int rcsa_pool_query(const void* q, int dtype, int64_t batch,
   if (!aligned16(q) || (q_i8 && (reinterpret_cast<uintptr_t>(q_i8) & 7u)))
     return RCSA_ERR_ALIGN;
   PoolArgs a{q, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, qhat,
-             nullptr, nullptr, nullptr, q_i8, q_scale, nullptr};
+             nullptr, nullptr, nullptr, q_i8, q_scale, nullptr, nullptr, 0};
   const int64_t nbh = batch * n_heads;
   if (dtype == RCSA_BF16) {
     if (q_i8) launch_pool<u16, true, false>(a, nbh, block_size, head_dim, stream);
@@ -497,7 +528,7 @@ extern "C" int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_
   if (!aligned16(k)) return RCSA_ERR_ALIGN;
   if (block_mask && (reinterpret_cast<uintptr_t>(block_mask) & 7u)) return RCSA_ERR_ALIGN;
   PoolArgs a{k, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, khat,
-             ksum, kmin, kmax, nullptr, nullptr, block_mask};
+             ksum, kmin, kmax, nullptr, nullptr, block_mask, nullptr, 0};
   const int64_t nbh = batch * n_heads;
   if (dtype == RCSA_BF16) {
     if (stats) launch_pool<u16, false, true>(a, nbh, block_size, head_dim, stream);
@@ -514,10 +545,17 @@ extern "C" int rcsa_pool_query_key(
     int64_t n_qblocks, int64_t n_kblocks, int64_t block_size, int64_t head_dim,
     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
     int64_t k_stride_h, int64_t k_stride_t, const uint8_t* q_valid, const uint8_t* k_valid,
-    float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum, float* kmin,
-    float* kmax, uint32_t* block_mask, hipStream_t stream) {
+    const int32_t* q_slot_token, int64_t q_src_len, const int32_t* k_slot_token,
+    int64_t k_src_len, float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum,
+    float* kmin, float* kmax, uint32_t* block_mask, hipStream_t stream) {
   if (!q || !k || !qhat || !q_i8 || !q_scale || !khat || !ksum || !kmin || !kmax)
     return RCSA_ERR_NULL;
+  // both gathered or neither (one kernel instance serves both tile kinds)
+  if ((q_slot_token == nullptr) != (k_slot_token == nullptr)) return RCSA_ERR_NULL;
+  const bool map = q_slot_token != nullptr;
+  if (map && (q_src_len <= 0 || k_src_len <= 0 || q_src_len >= (int64_t{1} << 31) ||
+              k_src_len >= (int64_t{1} << 31)))
+    return RCSA_ERR_SHAPE;
   int st = check_pool_shape(dtype, batch, n_heads, n_qblocks, block_size, head_dim,
                             q_stride_b, q_stride_h, q_stride_t);
   if (st) return st;
@@ -528,18 +566,21 @@ extern "C" int rcsa_pool_query_key(
     return RCSA_ERR_ALIGN;
   if (block_mask && (reinterpret_cast<uintptr_t>(block_mask) & 7u)) return RCSA_ERR_ALIGN;
   const PoolArgs qa{q, n_heads, n_qblocks, q_stride_b, q_stride_h, q_stride_t, q_valid, qhat,
-                    nullptr, nullptr, nullptr, q_i8, q_scale, nullptr};
+                    nullptr, nullptr, nullptr, q_i8, q_scale, nullptr, q_slot_token,
+                    q_src_len};
   const PoolArgs ka{k, n_heads, n_kblocks, k_stride_b, k_stride_h, k_stride_t, k_valid, khat,
-                    ksum, kmin, kmax, nullptr, nullptr, block_mask};
+                    ksum, kmin, kmax, nullptr, nullptr, block_mask, k_slot_token, k_src_len};
   const int64_t nbh = batch * n_heads;
   const int64_t q_tiles = nbh * n_qblocks;
   const dim3 grid(static_cast<unsigned>(q_tiles + nbh * n_kblocks)), block(kPoolThreads);
-#define RCSA_PQK(T_, D_, BS_) pool_qk_kernel<T_, D_, BS_><<<grid, block, 0, stream>>>(qa, ka, q_tiles)
+#define RCSA_PQK(T_, D_, BS_)                                                     \
+  if (map) pool_qk_kernel<T_, D_, BS_, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles); \
+  else pool_qk_kernel<T_, D_, BS_, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles)
 #define RCSA_PQK_T(T_)                                               \
-  if (head_dim == 128 && block_size == 128) RCSA_PQK(T_, 128, 128);  \
-  else if (head_dim == 128) RCSA_PQK(T_, 128, 64);                   \
-  else if (block_size == 128) RCSA_PQK(T_, 64, 128);                 \
-  else RCSA_PQK(T_, 64, 64);
+  if (head_dim == 128 && block_size == 128) { RCSA_PQK(T_, 128, 128); } \
+  else if (head_dim == 128) { RCSA_PQK(T_, 128, 64); }                  \
+  else if (block_size == 128) { RCSA_PQK(T_, 64, 128); }                \
+  else { RCSA_PQK(T_, 64, 64); }
   if (dtype == RCSA_BF16) { RCSA_PQK_T(u16) } else { RCSA_PQK_T(float) }
 #undef RCSA_PQK_T
 #undef RCSA_PQK
@@ -563,10 +604,12 @@ extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
                                  int64_t n_heads, int64_t n_blocks, int64_t block_size,
                                  int64_t head_dim, int64_t stride_b, int64_t stride_h,
                                  int64_t stride_t, const uint8_t* valid,
+                                 const int32_t* slot_token, int64_t src_len,
                                  const float* ksum, const float* kmin,
                                  const float* kmax, float* kmean, int8_t* k_i8,
                                  float* k_scale, hipStream_t stream) {
   if (!k || !ksum || !kmin || !kmax || !kmean || !k_i8 || !k_scale) return RCSA_ERR_NULL;
+  if (slot_token && (src_len <= 0 || src_len >= (int64_t{1} << 31))) return RCSA_ERR_SHAPE;
   int st = check_pool_shape(dtype, batch, n_heads, n_blocks, block_size, head_dim,
                             stride_b, stride_h, stride_t);
   if (st) return st;
@@ -574,16 +617,22 @@ extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
   const int64_t nbh = batch * n_heads;
   const int64_t n_tokens = n_blocks * block_size;
   if (head_dim == 128)
-    kmean_kernel<128><<<dim3(nbh * 8), dim3(256), 0, stream>>>(ksum, valid, n_blocks, n_tokens, kmean);
+    kmean_kernel<128><<<dim3(nbh * 8), dim3(256), 0, stream>>>(ksum, valid, slot_token, src_len,
+                                                               n_blocks, n_tokens, kmean);
   else
-    kmean_kernel<64><<<dim3(nbh * 4), dim3(256), 0, stream>>>(ksum, valid, n_blocks, n_tokens, kmean);
+    kmean_kernel<64><<<dim3(nbh * 4), dim3(256), 0, stream>>>(ksum, valid, slot_token, src_len,
+                                                              n_blocks, n_tokens, kmean);
   st = launch_status();
   if (st) return st;
   PoolArgs a{k, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, nullptr,
              const_cast<float*>(ksum), const_cast<float*>(kmin),
-             const_cast<float*>(kmax), nullptr, nullptr};
+             const_cast<float*>(kmax), nullptr, nullptr, nullptr, slot_token, src_len};
   dim3 grid(static_cast<unsigned>(nbh * n_blocks)), block(kPoolThreads);
-#define RCSA_QK(T, D, BS) quant_key_kernel<T, D, BS><<<grid, block, 0, stream>>>(a, kmean, k_i8, k_scale)
+#define RCSA_QK(T, D, BS)                                                                   \
+  do {                                                                                      \
+    if (slot_token) quant_key_kernel<T, D, BS, true><<<grid, block, 0, stream>>>(a, kmean, k_i8, k_scale); \
+    else quant_key_kernel<T, D, BS, false><<<grid, block, 0, stream>>>(a, kmean, k_i8, k_scale); \
+  } while (0)
   if (dtype == RCSA_BF16) {
     if (head_dim == 128 && block_size == 128) RCSA_QK(u16, 128, 128);
     else if (head_dim == 128) RCSA_QK(u16, 128, 64);

@@ -67,7 +67,18 @@ struct AttnArgs {
   int64_t n_bh, n_items, xcd_items, xcd_direct, n_split, n_tail;
   u16* ws_o;
   float2* ws_ml;
+  // Output scatter (nullable): packed query row r goes to row out_tok[r] of
+  // Out and M (out_len rows per (b, h)); -1 or a row >= out_len is dropped.
+  const int32_t* out_tok;
+  int64_t out_len;
 };
+
+// Output row of packed query row r, or -1 when the row is not written.
+__device__ __forceinline__ int64_t out_row(const AttnArgs& a, int64_t r) {
+  if (a.out_tok == nullptr) return r;
+  const int32_t t = a.out_tok[r];
+  return (t < 0 || t >= a.out_len) ? -1 : t;
+}
 
 constexpr float kTau = 8.0f;               // lazy-rescale threshold, log2 units
 constexpr float kMagicF = 12582912.0f;     // 1.5 * 2^23
@@ -741,10 +752,11 @@ sparse_attn_kernel(AttnArgs a) {
   const float inv = l > 0.0f ? 1.0f / l : 0.0f;
   fa *= inv;
   fb *= inv;
-  if (qrow_ok) {
-    // a share writes its normalised partial and (m, l) to the workspace
+  // a share writes its normalised partial and (m, l) to the workspace
+  const int64_t orow = qrow_ok && nsp == 1 ? out_row(a, qrow) : qrow;
+  if (qrow_ok && orow >= 0) {
     const int64_t ws_row = (split * a.n_tail + tail) * BM + (qrow - qb * BM);
-    u16* op = nsp == 1 ? a.out + b * a.soz + h * a.soh + qrow * a.som : a.ws_o + ws_row * D;
+    u16* op = nsp == 1 ? a.out + b * a.soz + h * a.soh + orow * a.som : a.ws_o + ws_row * D;
 #pragma unroll
     for (int dt = 0; dt < C::NDT; ++dt)
 #pragma unroll
@@ -764,7 +776,7 @@ sparse_attn_kernel(AttnArgs a) {
       if (nsp > 1) {
         a.ws_ml[ws_row] = make_float2(l > 0.0f ? m : -INFINITY, l);
       } else if (a.lse) {
-        a.lse[(b * a.H + h) * a.q_len + qrow] =
+        a.lse[(b * a.H + h) * (a.out_tok ? a.out_len : a.q_len) + orow] =
             l > 0.0f ? (m + __log2f(l)) * 0.69314718055994531f : -INFINITY;
       }
     }
@@ -790,6 +802,8 @@ attn_merge_kernel(AttnArgs a) {
   const int64_t qb = item % a.n_qblocks, bh = item / a.n_qblocks;
   const int64_t qrow = qb * a.block_m + r;
   if (qrow >= a.q_len) return;
+  const int64_t orow = out_row(a, qrow);
+  if (orow < 0) return;
   float mx = -INFINITY;
   for (int64_t s = 0; s < a.n_split; ++s) mx = fmaxf(mx, a.ws_ml[s * rows + trow].x);
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -808,12 +822,12 @@ attn_merge_kernel(AttnArgs a) {
   }
   const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
   const int64_t b = bh / a.H, h = bh % a.H;
-  u16* op = a.out + b * a.soz + h * a.soh + qrow * a.som + c * 8;
+  u16* op = a.out + b * a.soz + h * a.soh + orow * a.som + c * 8;
   *reinterpret_cast<uint4*>(op) =
       make_uint4(pack_bf16x2(acc[0] * inv, acc[1] * inv), pack_bf16x2(acc[2] * inv, acc[3] * inv),
                  pack_bf16x2(acc[4] * inv, acc[5] * inv), pack_bf16x2(acc[6] * inv, acc[7] * inv));
   if (a.lse && c == 0)
-    a.lse[bh * a.q_len + qrow] =
+    a.lse[bh * (a.out_tok ? a.out_len : a.q_len) + orow] =
         wsum > 0.0f ? (mx + __log2f(wsum)) * 0.69314718055994531f : -INFINITY;
 }
 
@@ -1009,7 +1023,7 @@ extern "C" int rcsa_sparse_attn_int8_split(
     int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
     int64_t BLOCK_N, int64_t max_k, int64_t n_split, void* workspace,
-    int64_t workspace_bytes, hipStream_t stream) {
+    int64_t workspace_bytes, const int32_t* out_token, int64_t out_len, hipStream_t stream) {
   if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -1027,6 +1041,11 @@ extern "C" int rcsa_sparse_attn_int8_split(
                        H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 16);
   if (st) return st;
   if (q_scale_stride < a.n_qblocks || k_scale_stride < a.n_kblocks) return RCSA_ERR_STRIDE;
+  if (out_token) {  // Out and M hold out_len rows per (b, h), written through the map
+    if (out_len <= 0 || out_len >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
+    a.out_tok = out_token;
+    a.out_len = out_len;
+  }
   if (K_block_mask) {  // the bits replace the validity bytes
     if (reinterpret_cast<uintptr_t>(K_block_mask) & 3u) return RCSA_ERR_ALIGN;
     a.kmask = K_block_mask;
@@ -1066,14 +1085,15 @@ extern "C" int rcsa_sparse_attn_int8(
     int64_t stride_oh, int64_t stride_om, int64_t stride_bz, int64_t stride_bh,
     int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
-    int64_t BLOCK_N, int64_t max_k, hipStream_t stream) {
+    int64_t BLOCK_N, int64_t max_k, const int32_t* out_token, int64_t out_len,
+    hipStream_t stream) {
   return rcsa_sparse_attn_int8_split(
       Q, q_scale, q_scale_stride, K, k_scale, k_scale_stride, V, K_valid, K_block_mask,
       sm_scale, M, Out,
       block_indices, block_indices_lens, stride_qz, stride_qh, stride_qm, stride_kz,
       stride_kh, stride_kn, stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
       stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B, H, Q_LEN, K_LEN,
-      HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, stream);
+      HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, out_token, out_len, stream);
 }
 
 extern "C" int64_t rcsa_attn_workspace_bytes(int64_t B, int64_t H, int64_t Q_LEN,

@@ -127,20 +127,59 @@ def pool_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
     return (khat, ksum, kmin, kmax, mask) if block_mask else (khat, ksum, kmin, kmax)
 
 
+def _slot_map(m: torch.Tensor, block_size: int, device, fn: str) -> torch.Tensor:
+    """int32 slot -> token map on ``device`` (-1 = empty slot), a whole number of blocks."""
+    if m.ndim != 1 or m.numel() == 0 or m.numel() % block_size:
+        raise ValueError(f"{fn}: slot map must be a vector of whole {block_size}-slot blocks")
+    if m.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"{fn}: slot map must be int32 or int64")
+    return m.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _tokens_bhld(x: torch.Tensor, slots: torch.Tensor, block_size: int, fn: str):
+    """Shape of a gathered source ``[B, L, H, D]``: (B, H, n_slots, D, n_blocks, L, strides)."""
+    if x.ndim != 4 or x.stride(3) != 1:
+        raise ValueError(f"{fn}: a gathered source must be [B, L, H, D] with a contiguous last dim")
+    B, L, H, D = x.shape
+    n = slots.numel()
+    return B, H, n, D, n // block_size, L, (x.stride(0), x.stride(2), x.stride(1))
+
+
 def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Tensor,
-                   k_valid: Optional[torch.Tensor], block_size: int):
+                   k_valid: Optional[torch.Tensor], block_size: int, *,
+                   q_slot_token: Optional[torch.Tensor] = None,
+                   k_slot_token: Optional[torch.Tensor] = None):
     """``pool_query(q, q_valid, quantize=True)`` and ``pool_key(k, k_valid, stats=True,
     block_mask=True)`` in one launch (no reference counterpart: the int8 layer call's
     pooling pass).  Returns ``(qhat, q_i8, q_scale, khat, ksum, kmin, kmax, block_mask)``,
     bit for bit the two calls' outputs.
+
+    With ``q_slot_token`` / ``k_slot_token`` (both or neither) q and k are token-major
+    ``[B, L, H, D]`` sources gathered on the fly: the outputs equal those of
+    ``pool_query_key(pack_tokens(q, q_slot_token), ..., pack_tokens(k, k_slot_token), ...)``
+    (the q[:, flat] / k[:, flat] gathers of
+    P/matrix_curvature_phase_frame_weave.py:5677-5684 fused into the pass); the valid
+    masks, when given, stay per packed slot.
     """
     fn = "pool_query_key"
     _require_cuda(fn, q, k)
     code = _dtype_code(q, fn)
     if _dtype_code(k, fn) != code:
         raise TypeError(f"{fn}: q and k must share a dtype")
-    B, H, Lq, D, NQ = _bhld(q, block_size, fn)
-    Bk, Hk, Lk, Dk, NK = _bhld(k, block_size, fn)
+    if (q_slot_token is None) != (k_slot_token is None):
+        raise ValueError(f"{fn}: give both slot maps or neither")
+    if q_slot_token is not None:
+        qm = _slot_map(q_slot_token, block_size, q.device, fn)
+        km = _slot_map(k_slot_token, block_size, k.device, fn)
+        B, H, Lq, D, NQ, q_src, q_strides = _tokens_bhld(q, qm, block_size, fn)
+        Bk, Hk, Lk, Dk, NK, k_src, k_strides = _tokens_bhld(k, km, block_size, fn)
+    else:
+        qm = km = None
+        q_src = k_src = 0
+        B, H, Lq, D, NQ = _bhld(q, block_size, fn)
+        Bk, Hk, Lk, Dk, NK = _bhld(k, block_size, fn)
+        q_strides = (q.stride(0), q.stride(1), q.stride(2))
+        k_strides = (k.stride(0), k.stride(1), k.stride(2))
     if (Bk, Hk, Dk) != (B, H, D):
         raise ValueError(f"{fn}: q {tuple(q.shape)} and k {tuple(k.shape)} differ in B, H or D")
     qv = _valid_u8(q_valid, Lq, q.device, fn)
@@ -152,9 +191,9 @@ def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Te
     khat, ksum, kmin, kmax = (torch.empty(B * H, NK, D, **f32) for _ in range(4))
     mask = torch.empty(NK, block_size // 32, device=k.device, dtype=torch.int32)
     st = _lib.load().rcsa_pool_query_key(
-        q.data_ptr(), k.data_ptr(), code, B, H, NQ, NK, block_size, D,
-        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
-        _ptr(qv), _ptr(kv), qhat.data_ptr(), q_i8.data_ptr(), q_scale.data_ptr(),
+        q.data_ptr(), k.data_ptr(), code, B, H, NQ, NK, block_size, D, *q_strides, *k_strides,
+        _ptr(qv), _ptr(kv), _ptr(qm), q_src, _ptr(km), k_src,
+        qhat.data_ptr(), q_i8.data_ptr(), q_scale.data_ptr(),
         khat.data_ptr(), ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), mask.data_ptr(),
         _stream())
     check(st, fn)
@@ -251,15 +290,24 @@ def select_topk(score: torch.Tensor, k, *, forced: Optional[torch.Tensor] = None
 
 
 def quantize_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,
-                 ksum: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor):
+                 ksum: torch.Tensor, kmin: torch.Tensor, kmax: torch.Tensor, *,
+                 slot_token: Optional[torch.Tensor] = None):
     """Per-head mean-smoothed, per-block symmetric int8 keys.
 
-    Returns ``(k_i8 [B, H, L, D], k_scale [B*H, NB], kmean [B*H, D])``.
+    Returns ``(k_i8 [B, H, L, D], k_scale [B*H, NB], kmean [B*H, D])``.  With
+    ``slot_token`` k is a token-major ``[B, L_tokens, H, D]`` source gathered on the
+    fly (as in :func:`pool_query_key`); k_i8 stays packed ``[B, H, n_slots, D]``.
     """
     fn = "quantize_key"
     _require_cuda(fn, k, ksum, kmin, kmax)
     code = _dtype_code(k, fn)
-    B, H, L, D, NB = _bhld(k, block_size, fn)
+    if slot_token is not None:
+        sm = _slot_map(slot_token, block_size, k.device, fn)
+        B, H, L, D, NB, src_len, strides = _tokens_bhld(k, sm, block_size, fn)
+    else:
+        sm, src_len = None, 0
+        B, H, L, D, NB = _bhld(k, block_size, fn)
+        strides = (k.stride(0), k.stride(1), k.stride(2))
     for t in (ksum, kmin, kmax):
         if t.shape != (B * H, NB, D) or t.dtype != torch.float32 or not t.is_contiguous():
             raise ValueError(f"{fn}: statistics must be contiguous float32 [{B * H}, {NB}, {D}]")
@@ -268,8 +316,9 @@ def quantize_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int
     k_i8 = torch.empty(B, H, L, D, device=k.device, dtype=torch.int8)
     k_scale = torch.empty(B * H, NB, device=k.device, dtype=torch.float32)
     st = _lib.load().rcsa_quantize_key(
-        k.data_ptr(), code, B, H, NB, block_size, D, k.stride(0), k.stride(1), k.stride(2),
-        _ptr(v), ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(),
+        k.data_ptr(), code, B, H, NB, block_size, D, *strides,
+        _ptr(v), _ptr(sm), src_len, ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(),
+        kmean.data_ptr(),
         k_i8.data_ptr(), k_scale.data_ptr(), _stream())
     check(st, fn)
     return k_i8, k_scale, kmean
@@ -351,12 +400,15 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
 
 def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=None, *,
                      block_m=128, block_n=128, sm_scale=None, return_lse=False, out=None,
-                     n_split=None, block_mask=None):
+                     n_split=None, block_mask=None, out_token=None, out_len=None):
     """int8-QK / bf16-PV block-sparse attention over quantiser outputs.
 
     ``block_mask`` (int32 ``[ceil(Lk / block_n), block_n // 32]``, e.g. from
     ``pool_key(..., block_mask=True)``) gives the key validity as bits and
-    replaces ``valid``."""
+    replaces ``valid``.  ``out_token`` (a slot -> token map of the packed queries)
+    scatters the output into a token-major ``[B, out_len, H, D]`` tensor (and the
+    LSE into ``[B, H, out_len]``): ``unpack_tokens`` fused into the epilogue
+    (P/matrix_curvature_phase_frame_weave.py:6095).  Every token must own a slot."""
     fn = "sparse_attn_int8"
     _require_cuda(fn, q_i8, q_scale, k_i8, k_scale, v, indices, counts)
     _attn_common(q_i8, k_i8, v, indices, counts, fn)
@@ -385,9 +437,23 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         kv = None
     else:
         kv = _valid_u8(valid, Lk, q_i8.device, fn)
-    if out is None:
-        out = torch.empty(B, H, Lq, D, device=q_i8.device, dtype=torch.bfloat16)
-    lse = torch.empty(B, H, Lq, device=q_i8.device, dtype=torch.float32) if return_lse else None
+    if out_token is not None:
+        om = _slot_map(out_token, block_m, q_i8.device, fn)
+        if om.numel() < Lq or out_len is None or int(out_len) <= 0:
+            raise ValueError(f"{fn}: out_token needs {Lq} slots and a positive out_len")
+        n_out = int(out_len)
+        if out is None:
+            out = torch.empty(B, n_out, H, D, device=q_i8.device, dtype=torch.bfloat16)
+        if out.shape != (B, n_out, H, D) or out.dtype != torch.bfloat16 or out.stride(3) != 1:
+            raise ValueError(f"{fn}: out must be bfloat16 [{B}, {n_out}, {H}, {D}]")
+        o_strides = (out.stride(0), out.stride(2), out.stride(1))
+    else:
+        om, n_out = None, 0
+        if out is None:
+            out = torch.empty(B, H, Lq, D, device=q_i8.device, dtype=torch.bfloat16)
+        o_strides = (out.stride(0), out.stride(1), out.stride(2))
+    lse = (torch.empty(B, H, n_out if om is not None else Lq, device=q_i8.device,
+                       dtype=torch.float32) if return_lse else None)
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q_i8.device, fn)
     st = _lib.load().rcsa_sparse_attn_int8_split(
@@ -397,10 +463,11 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         out.data_ptr(), indices.data_ptr(), counts.data_ptr(),
         q_i8.stride(0), q_i8.stride(1), q_i8.stride(2),
         k_i8.stride(0), k_i8.stride(1), k_i8.stride(2),
-        v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
+        v.stride(0), v.stride(1), v.stride(2), *o_strides,
         indices.stride(0), indices.stride(1), indices.stride(2),
         counts.stride(0), counts.stride(1), counts.stride(2),
-        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _stream())
+        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _ptr(om),
+        n_out, _stream())
     check(st, fn)
     return (out, lse) if return_lse else out
 

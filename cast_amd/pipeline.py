@@ -57,7 +57,9 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    allowed: Optional[torch.Tensor] = None, int8: bool = True,
                    max_k: Optional[int] = None, sm_scale: Optional[float] = None,
                    return_lse: bool = False, order: str = "index",
-                   n_split: Optional[int] = None, overlap: bool = True) -> RCSAResult:
+                   n_split: Optional[int] = None, overlap: bool = True,
+                   q_slot_token: Optional[torch.Tensor] = None,
+                   k_slot_token: Optional[torch.Tensor] = None) -> RCSAResult:
     """One RCSA layer call over packed Q/K/V ``[B, H, NB*BS, D]`` (bf16 or fp32).
 
     ``k_select`` is the per-row number of key blocks handed to attention
@@ -68,9 +70,27 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     that many workgroups (None: chosen from the device's compute-unit count).
     ``overlap`` runs the scores and the top-k on a side stream beside the
     int8 key pass (int8 only; results are identical either way).
+
+    ``q_slot_token`` / ``k_slot_token`` (int8 only, both or neither; e.g. a
+    ``CompactLayout.slot_token``): q, k and v are token-major ``[B, L, H, D]``
+    and the packing happens inside the kernels.  The pooling pass and the key
+    quantiser gather Q/K rows through the maps, V is packed once, and the
+    attention writes its output (and LSE) straight to the token rows, so
+    ``out`` is ``[B, Lq_tokens, H, D]``.  The results equal those of the packed
+    call on ``pack_tokens`` inputs followed by ``unpack_tokens``.
     """
-    B, H, Lq, D = q.shape
-    Lk = k.shape[2]
+    gathered = q_slot_token is not None or k_slot_token is not None
+    if gathered:
+        if q_slot_token is None or k_slot_token is None:
+            raise ValueError("rcsa_attention: give both slot maps or neither")
+        if not int8:
+            raise ValueError("rcsa_attention: gathered inputs need the int8 path")
+        B, _, H, D = q.shape
+        Lq, Lk = q_slot_token.numel(), k_slot_token.numel()
+        v = ops.pack_tokens(v, k_slot_token)  # V is read by the attention only
+    else:
+        B, H, Lq, D = q.shape
+        Lk = k.shape[2]
     bs = block_size
     main = torch.cuda.current_stream(q.device) if q.is_cuda else None
     # the bf16 path has no key pass left to overlap with
@@ -84,7 +104,7 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
 
     if int8:  # one launch pools Q (+ int8) and K (+ stats and validity bits)
         qhat, q_i8, q_scale, khat, ksum, kmin, kmax, k_mask = ops.pool_query_key(
-            q, q_valid, k, k_valid, bs)
+            q, q_valid, k, k_valid, bs, q_slot_token=q_slot_token, k_slot_token=k_slot_token)
     else:
         qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs)
         khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs)
@@ -104,7 +124,8 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     lse = None
     if int8:
-        k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax)
+        k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax,
+                                                slot_token=k_slot_token)
     if side is not None:
         main.wait_stream(side)  # the selection
         # No record_stream: the side stream is private to this function and
@@ -115,7 +136,9 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         res = ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v if v.dtype == torch.bfloat16
                                    else v.to(torch.bfloat16), idx4, cnt3, None,
                                    block_m=bs, block_n=bs, sm_scale=scale,
-                                   return_lse=return_lse, n_split=n_split, block_mask=k_mask)
+                                   return_lse=return_lse, n_split=n_split, block_mask=k_mask,
+                                   out_token=q_slot_token if gathered else None,
+                                   out_len=q.shape[1] if gathered else None)
     else:
         k_i8 = k_scale = kmean = None
         qb = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)

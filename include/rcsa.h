@@ -100,13 +100,24 @@ int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
  * pooling pass, so the short query pass runs inside the key pass instead of
  * before it.  Q and K share dtype, batch, heads, block_size and head_dim; each
  * has its own block count, strides and validity.
+ *
+ * Gathered inputs (both maps non-NULL, or both NULL): q and k are then
+ * token-major sources (e.g. [B, L, H, D] with stride_t = H * D) and packed
+ * slot s = block * block_size + r reads token slot_token[s] of the source
+ * (q_src_len / k_src_len tokens); -1, or a token >= src_len, is an empty
+ * (invalid) slot.  The outputs are those of rcsa_pack_tokens followed by the
+ * ungathered call, bit for bit, without the packed copies.  Fuses the
+ * q[:, flat] / k[:, flat] gathers of P/matrix_curvature_phase_frame_weave.py:5677-5684
+ * into the pooling pass; q_valid / k_valid, when given, stay per packed slot.
  */
 int rcsa_pool_query_key(const void* q, const void* k, int dtype, int64_t batch,
                         int64_t n_heads, int64_t n_qblocks, int64_t n_kblocks,
                         int64_t block_size, int64_t head_dim, int64_t q_stride_b,
                         int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
                         int64_t k_stride_h, int64_t k_stride_t, const uint8_t* q_valid,
-                        const uint8_t* k_valid, float* qhat, int8_t* q_i8, float* q_scale,
+                        const uint8_t* k_valid, const int32_t* q_slot_token,
+                        int64_t q_src_len, const int32_t* k_slot_token, int64_t k_src_len,
+                        float* qhat, int8_t* q_i8, float* q_scale,
                         float* khat, float* ksum, float* kmin, float* kmax,
                         uint32_t* block_mask, hipStream_t stream);
 
@@ -151,11 +162,14 @@ int rcsa_select_topk(const float* score, int64_t n_bh, int64_t n_qblocks,
  *   k_i8[bh, t, c]  = clamp(rne((k - kmean) / k_scale), -127, 127), 0 on invalid tokens
  * Softmax is invariant to the per-row constant q . kmean, so attention over
  * the smoothed keys equals attention over the original keys.
+ * slot_token (nullable): gathered keys, as for rcsa_pool_query_key (k is the
+ * token-major source of src_len tokens; k_i8 stays packed).
  */
 int rcsa_quantize_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
                       int64_t n_blocks, int64_t block_size, int64_t head_dim,
                       int64_t stride_b, int64_t stride_h, int64_t stride_t,
-                      const uint8_t* valid, const float* ksum,
+                      const uint8_t* valid, const int32_t* slot_token, int64_t src_len,
+                      const float* ksum,
                       const float* kmin, const float* kmax, float* kmean,
                       int8_t* k_i8, float* k_scale, hipStream_t stream);
 
@@ -202,6 +216,11 @@ int rcsa_sparse_attn_bf16(const void* Q, const void* K, const void* V,
  * [ceil(K_LEN/BLOCK_N)][BLOCK_N / 32] in rcsa_pool_key's block_mask form;
  * when given it replaces K_valid (which may then be NULL) and the kernel
  * reads it with scalar loads instead of staging validity bytes.
+ * out_token (nullable): output scatter.  Row r of the packed query writes row
+ * out_token[r] of Out and M, which then hold out_len rows per (b, h) (e.g. a
+ * token-major [B, L, H, D] Out with stride_om = H * D); -1, or a row >=
+ * out_len, is not written.  Fuses output_packed[:, token_to_packed]
+ * (P/matrix_curvature_phase_frame_weave.py:6095) into the epilogue.
  */
 int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
                           int64_t q_scale_stride, const int8_t* K,
@@ -218,7 +237,8 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
                           int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
                           int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
                           int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
-                          int64_t max_k, hipStream_t stream);
+                          int64_t max_k, const int32_t* out_token, int64_t out_len,
+                          hipStream_t stream);
 
 /*
  * Split-list variants of the two attention entry points (same arguments,
@@ -265,7 +285,8 @@ int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
                                 int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
                                 int64_t max_k, int64_t n_split, void* workspace,
-                                int64_t workspace_bytes, hipStream_t stream);
+                                int64_t workspace_bytes, const int32_t* out_token,
+                                int64_t out_len, hipStream_t stream);
 
 /* Workspace bytes of a split launch on the current device, an upper bound
  * for BLOCK_M in {64, 128} (0 for n_split == 1, -1 on bad sizes). */
