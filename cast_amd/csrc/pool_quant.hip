@@ -30,12 +30,14 @@ struct PoolArgs {
   int64_t src_len;
 };
 
-// Source row of packed row r of block blk: the row itself, or through the
-// gather map (an empty slot reads token 0, which its validity then drops).
+// Source of packed row r of block blk, relative to the tile base (x advanced
+// to the block's first row without a map, the (b, h) plane with one): the
+// row itself, or through the gather map (an empty slot reads token 0, which
+// its validity then drops).
 template <bool MAP, int BS>
 __device__ __forceinline__ int64_t src_row(const PoolArgs& a, int64_t blk, int r) {
   if constexpr (!MAP) {
-    return blk * BS + r;
+    return r;
   } else {
     const int32_t tk = a.slot_tok[blk * BS + r];
     return (tk < 0 || tk >= a.src_len) ? 0 : tk;
@@ -98,6 +100,11 @@ template <>
 struct Raw8<u16> {
   uint4 w;
   __device__ __forceinline__ void load(const u16* p) { w = *reinterpret_cast<const uint4*>(p); }
+  // Hide the words from value reuse: a second get() then converts again
+  // instead of keeping the first pass's floats alive.
+  __device__ __forceinline__ void opaque() {
+    asm volatile("" : "+v"(w.x), "+v"(w.y), "+v"(w.z), "+v"(w.w));
+  }
   __device__ __forceinline__ void get(float* out) const {
     const uint32_t v[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
@@ -113,6 +120,10 @@ struct Raw8<float> {
   __device__ __forceinline__ void load(const float* p) {
     a = reinterpret_cast<const float4*>(p)[0];
     b = reinterpret_cast<const float4*>(p)[1];
+  }
+  __device__ __forceinline__ void opaque() {
+    asm volatile("" : "+v"(a.x), "+v"(a.y), "+v"(a.z), "+v"(a.w));
+    asm volatile("" : "+v"(b.x), "+v"(b.y), "+v"(b.z), "+v"(b.w));
   }
   __device__ __forceinline__ void get(float* out) const {
     out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
@@ -142,7 +153,8 @@ __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
   const int64_t blk = tile % a.n_blocks;
   const int64_t bh = tile / a.n_blocks;
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
-  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h;
+  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
+               (MAP ? 0 : blk * BS * a.stride_t);
   const int t = threadIdx.x;
   const int c = t % CPR, g = t / CPR;
   const int lane = t % kWave, wave = t / kWave;
@@ -234,6 +246,7 @@ __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
       uint32_t lo = 0, hi = 0;
       if (s_valid[r]) {
         float v[8];
+        raw[i].opaque();
         raw[i].get(v);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -414,7 +427,8 @@ quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
   const int t = threadIdx.x;
   const int c = t % CPR, g = t / CPR;
-  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h;
+  const T* x = static_cast<const T*>(a.x) + b_outer * a.stride_b + h * a.stride_h +
+               (MAP ? 0 : blk * BS * a.stride_t);
   Raw8<T> raw[ROWS];
 #pragma unroll
   for (int i = 0; i < ROWS; ++i)
