@@ -368,6 +368,15 @@ def main() -> int:
                                           "effective_TOPS": sweep_ops / step_ms / 1e9}
         del layers
         extras["compact_layout_call"] = compact_layout_call(args.seed, iters)
+        # per-row budgets on the device: 30 layers x 28 query blocks, and one
+        # 853-row section (the longest history), largest remainder + saturation
+        gb = torch.Generator(device=dev).manual_seed(args.seed)
+        w30 = torch.rand(30, 28, device=dev, generator=gb)
+        w853 = torch.rand(1, 853, device=dev, generator=gb)
+        extras["row_budgets_us"] = {
+            "30x28": 1e3 * _events_time(lambda: ops.row_budgets(w30, 28 * 69, cap=303), iters),
+            "1x853": 1e3 * _events_time(lambda: ops.row_budgets(w853, 853 * 64, cap=853),
+                                        iters)}
 
     line["extras"] = extras
     if not args.no_cpu_baseline:

@@ -17,7 +17,7 @@ from ._lib import RCSA_BF16, RCSA_F32, RCSA_ORDER_INDEX, RCSA_ORDER_RANK, check
 
 __all__ = [
     "pool_query", "pool_key", "block_scores", "select_topk", "quantize_key",
-    "sparse_attn_bf16", "sparse_attn_int8", "pack_tokens", "unpack_tokens",
+    "sparse_attn_bf16", "sparse_attn_int8", "pack_tokens", "unpack_tokens", "row_budgets",
 ]
 
 
@@ -198,6 +198,26 @@ def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Te
         _stream())
     check(st, fn)
     return qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask
+
+
+def row_budgets(weights: torch.Tensor, total_per_section: int, *, cap: int = 0,
+                target_total: Optional[int] = None) -> torch.Tensor:
+    """Per-row budgets on the device: ``budget.apportion_section_matrix(weights, total)``
+    and, with ``cap > 0``, ``budget.saturate(row, cap, target_total)`` on every section
+    row (P/qk_uncertainty_tangent_attention.py:847-865, 1239-1264;
+    P/matrix_curvature_phase_frame_weave.py:5807-5817).  ``weights`` is float32
+    ``[sections, n]`` on the GPU; returns int32 ``[sections, n]`` without a host sync."""
+    fn = "row_budgets"
+    _require_cuda(fn, weights)
+    if weights.ndim != 2 or weights.dtype != torch.float32 or weights.stride(1) != 1:
+        raise ValueError(f"{fn}: weights must be float32 [sections, n] with contiguous rows")
+    S, n = weights.shape
+    out = torch.empty(S, n, device=weights.device, dtype=torch.int32)
+    check(_lib.load().rcsa_row_budgets(weights.data_ptr(), S, n, weights.stride(0),
+                                       int(total_per_section), int(cap),
+                                       int(target_total) if target_total is not None else 0,
+                                       out.data_ptr(), n, _stream()), fn)
+    return out
 
 
 def block_scores(qhat: torch.Tensor, khat: torch.Tensor) -> torch.Tensor:

@@ -122,6 +122,25 @@ int rcsa_pool_query_key(const void* q, const void* k, int dtype, int64_t batch,
                         uint32_t* block_mask, hipStream_t stream);
 
 /*
+ * Per-row key-block budgets on the device, so no budget is read back to the
+ * host.  For every section row s of weights [n_sections][n] (row stride
+ * weights_stride): largest-remainder apportionment of total_per_section edges
+ * by max(w, 0) in fp32 (raw = total * w / sum w, floors, one more edge to the
+ * largest fractional parts, ties to the lower index; a row whose weights sum
+ * to <= 0 weighs every entry 1), as P/qk_uncertainty_tangent_attention.py:847-865
+ * and :1239-1264 (_apportion_section_matrix).  With cap > 0 every degree is
+ * then clamped to cap and the lost edges go, one each and pass after pass, to
+ * the lowest-index rows below cap until the row sums to target_total (<= 0:
+ * total_per_section) or no row has room, as the saturation at
+ * P/matrix_curvature_phase_frame_weave.py:5807-5817.  n <= 8192,
+ * total_per_section < 2^24.  degrees: int32 [n_sections][degrees_stride].
+ */
+int rcsa_row_budgets(const float* weights, int64_t n_sections, int64_t n,
+                     int64_t weights_stride, int64_t total_per_section, int64_t cap,
+                     int64_t target_total, int32_t* degrees, int64_t degrees_stride,
+                     hipStream_t stream);
+
+/*
  * Cosine block scores score[bh, i, j] = <qhat[bh, i], khat[bh, j]>.
  * Replaces torch.matmul(q_content, k_content.transpose(-2, -1)) at
  * P/matrix_curvature_phase_frame_weave.py:5701 and

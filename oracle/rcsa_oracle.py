@@ -19,6 +19,8 @@ docstring; the pins live in tests/test_oracle_pins.py:
                       per-row shift invariance of softmax
   compact_layout      reference's loop branch restated with pure-Python lists
   apportion*          exact rational arithmetic (fractions.Fraction) + conserved sums
+  saturate            closed forms: the result sums to min(target, n * cap), never
+                      exceeds cap, and only rows below cap before a pass gain
 """
 from __future__ import annotations
 
@@ -32,7 +34,7 @@ __all__ = [
     "pool_blocks", "block_scores", "local_stencil", "select_topk", "topk_margin",
     "quantize_query_blocks", "key_mean", "quantize_key_blocks", "dequantize_blocks",
     "sparse_attention", "sparse_attention_int8", "equivalence_stats", "compact_layout",
-    "apportion", "apportion_section_matrix", "budget_blocks", "rcsa_layer",
+    "apportion", "apportion_section_matrix", "saturate", "budget_blocks", "rcsa_layer",
 ]
 
 
@@ -381,6 +383,28 @@ def apportion(weights: Sequence[float], total: int) -> list[int]:
 def apportion_section_matrix(weights: Sequence[Sequence[float]], total_per_section: int):
     """Row-wise largest remainder (P/qk_uncertainty_tangent_attention.py:1239-1264)."""
     return [apportion(row, total_per_section) for row in weights]
+
+
+def saturate(degrees: Sequence[int], cap: int, target_total: int) -> list[int]:
+    """Clamp every row to ``cap``, then give the lost edges one each to the
+    lowest-index rows below ``cap``, pass after pass, until ``target_total`` or
+    no room is left (P/matrix_curvature_phase_frame_weave.py:5807-5817),
+    with Python ints one edge at a time.
+    """
+    d = [min(int(x), cap) for x in degrees]
+    missing = int(target_total) - sum(d)
+    while missing > 0:
+        gave = 0
+        for i in range(len(d)):
+            if missing == 0:
+                break
+            if d[i] < cap:
+                d[i] += 1
+                missing -= 1
+                gave += 1
+        if gave == 0:
+            break
+    return d
 
 
 def budget_blocks(fraction: float, n_history_blocks: int) -> int:

@@ -503,3 +503,29 @@ def test_rcsa_layer_composes_the_pinned_parts():
         for i in range(res["indices"].shape[1]):
             sel = set(res["indices"][r, i].tolist())
             assert set(range(nh, w.n_kblocks)) <= sel
+
+
+def test_saturate_pins():
+    """Oracle saturation against its closed forms on random rows: the result sums
+    to min(target, n * cap), never exceeds cap, keeps every row that was at or
+    below cap at least where it was, and fills the lowest-index rows first (a
+    row only gains when every lower row with room gained at least as much)."""
+    import random
+    rnd = random.Random(7)
+    for _ in range(300):
+        n = rnd.randint(1, 30)
+        cap = rnd.randint(1, 12)
+        deg = [rnd.randint(0, 20) for _ in range(n)]
+        target = rnd.randint(0, 25 * n)
+        got = orc.saturate(deg, cap, target)
+        clamped = [min(x, cap) for x in deg]
+        assert sum(got) == max(sum(clamped), min(target, n * cap))
+        assert all(g <= cap for g in got)
+        assert all(g >= c for g, c in zip(got, clamped))
+        gain = [g - c for g, c in zip(got, clamped)]
+        for i in range(n):
+            for j in range(i):
+                if clamped[j] + gain[j] < cap:  # row j still had room at the end
+                    assert gain[j] >= gain[i]
+    # a hand case: 2 edges lost to the cap go to rows 1 and 2
+    assert orc.saturate([12, 1, 1], 10, 14) == [10, 2, 2]
