@@ -58,7 +58,7 @@ __device__ __forceinline__ float block_sum_fixed(float v, float* s_tmp) {
 __global__ void __launch_bounds__(kBudgetThreads)
 apportion_kernel(const float* weights, int64_t ldw, int n, int total, int cap, int target,
                  int32_t* degrees, int64_t ldd) {
-  __shared__ float s_frac[kBudgetMaxN];
+  __shared__ __attribute__((aligned(16))) float s_frac[kBudgetMaxN];
   __shared__ int s_deg[kBudgetMaxN];
   __shared__ float s_f[4];
   __shared__ int s_i[4];
@@ -94,14 +94,22 @@ apportion_kernel(const float* weights, int64_t ldw, int n, int total, int cap, i
   const int rem = total - fl_sum;
 
   // one extra edge to the `rem` largest fractional parts, ties to the lower index
+  // (rank = entries ahead of i in that order; a straight count over 16-byte
+  // LDS reads, unrolled so the reads stay in flight)
   if (rem > 0) {
+    const int n4 = n & ~3;
     for (int i = lo; i < hi; ++i) {
       const float fi = s_frac[i];
       int rank = 0;
-      for (int j = 0; j < n && rank < rem; ++j) {
-        const float fj = s_frac[j];
-        rank += (fj > fi) || (fj == fi && j < i);
+#pragma unroll 4
+      for (int j = 0; j < n4; j += 4) {
+        const float4 f = *reinterpret_cast<const float4*>(&s_frac[j]);
+        rank += (f.x > fi) || (f.x == fi && j < i);
+        rank += (f.y > fi) || (f.y == fi && j + 1 < i);
+        rank += (f.z > fi) || (f.z == fi && j + 2 < i);
+        rank += (f.w > fi) || (f.w == fi && j + 3 < i);
       }
+      for (int j = n4; j < n; ++j) rank += (s_frac[j] > fi) || (s_frac[j] == fi && j < i);
       s_deg[i] += rank < rem;
     }
   }
