@@ -238,7 +238,8 @@ int rcsa_sparse_attn_bf16(const void* Q, const void* K, const void* V,
  * out_token (nullable): output scatter.  Row r of the packed query writes row
  * out_token[r] of Out and M, which then hold out_len rows per (b, h) (e.g. a
  * token-major [B, L, H, D] Out with stride_om = H * D); -1, or a row >=
- * out_len, is not written.  Fuses output_packed[:, token_to_packed]
+ * out_len, is not written, and no row may appear twice.  Rows of Out that no
+ * slot maps to are left as they were.  Fuses output_packed[:, token_to_packed]
  * (P/matrix_curvature_phase_frame_weave.py:6095) into the epilogue.
  */
 int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
