@@ -27,6 +27,9 @@ SIGNATURES: dict[str, list] = {
     "rcsa_pool_query_key": [_P, _P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                             _P, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
     "rcsa_block_scores": [_P, _P, _I, _I, _I, _I, _P, _P],
+    "rcsa_quantize_key_select": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I,
+                                 _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P,
+                                 _I, _P, _I, _P, _P],
     "rcsa_row_budgets": [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P],
     "rcsa_select_topk": [_P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _P, _I, _P, c_int, _P],
     "rcsa_quantize_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P,

@@ -5,6 +5,7 @@
 // once with 16-byte coalesced loads (a bf16 row of 128 channels is 16 lanes
 // x 16 B).  Per-channel partial sums are combined through LDS.
 #include "rcsa_common.h"
+#include "select_core.h"
 
 namespace rcsa {
 
@@ -414,16 +415,16 @@ kmean_kernel(const float* ksum, const uint8_t* valid, const int32_t* slot_tok,
 // loads are issued first; the scale (from the block's min/max and the head
 // mean) is computed while they are in flight.
 template <typename T, int D, int BS, bool MAP>
-__global__ void __launch_bounds__(kPoolThreads)
-quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
+__device__ __forceinline__ void quant_tile(const PoolArgs& a, const float* kmean, int8_t* k_i8,
+                                           float* k_scale, int64_t tile) {
   constexpr int CPR = D / 8;
   constexpr int RG = kPoolThreads / CPR;
   constexpr int ROWS = BS / RG;
   __shared__ float s_mean[D];
   __shared__ uint8_t s_valid[BS];
   __shared__ float s_red[4];
-  const int64_t blk = blockIdx.x % a.n_blocks;
-  const int64_t bh = blockIdx.x / a.n_blocks;
+  const int64_t blk = tile % a.n_blocks;
+  const int64_t bh = tile / a.n_blocks;
   const int64_t b_outer = bh / a.n_heads, h = bh % a.n_heads;
   const int t = threadIdx.x;
   const int c = t % CPR, g = t / CPR;
@@ -471,6 +472,26 @@ quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
     }
     *reinterpret_cast<uint2*>(out + r * D + c * 8) = make_uint2(lo, hi);
   }
+}
+
+template <typename T, int D, int BS, bool MAP>
+__global__ void __launch_bounds__(kPoolThreads)
+quant_key_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale) {
+  quant_tile<T, D, BS, MAP>(a, kmean, k_i8, k_scale, blockIdx.x);
+}
+
+// The key quantiser and the block scores + top-k selection in one launch: the
+// first n_sel workgroups each score and select kSelWaves rows (latency-bound
+// work that then runs inside the HBM-bound key pass), the rest quantise key
+// tiles.  No reference counterpart; replaces a side stream and its two
+// cross-stream waits.
+template <typename T, int D, int BS, bool MAP, int PER>
+__global__ void __launch_bounds__(kPoolThreads)
+quant_select_kernel(PoolArgs a, const float* kmean, int8_t* k_i8, float* k_scale, SelArgs sel,
+                    int64_t n_sel) {
+  static_assert(kSelWaves * kWave == kPoolThreads, "one block shape");
+  if (blockIdx.x < n_sel) select_rows<PER, false, true>(sel, blockIdx.x, nullptr);
+  else quant_tile<T, D, BS, MAP>(a, kmean, k_i8, k_scale, blockIdx.x - n_sel);
 }
 
 // ---------------------------------------------------------------------------
@@ -614,15 +635,18 @@ extern "C" int rcsa_block_scores(const float* qhat, const float* khat, int64_t n
   return launch_status();
 }
 
-extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
-                                 int64_t n_heads, int64_t n_blocks, int64_t block_size,
-                                 int64_t head_dim, int64_t stride_b, int64_t stride_h,
-                                 int64_t stride_t, const uint8_t* valid,
-                                 const int32_t* slot_token, int64_t src_len,
-                                 const float* ksum, const float* kmin,
-                                 const float* kmax, float* kmean, int8_t* k_i8,
-                                 float* k_scale, hipStream_t stream) {
+// The key mean, then the quantiser (with sel: fused with the scores + top-k).
+static int quantize_key_impl(const void* k, int dtype, int64_t batch, int64_t n_heads,
+                             int64_t n_blocks, int64_t block_size, int64_t head_dim,
+                             int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                             const uint8_t* valid, const int32_t* slot_token, int64_t src_len,
+                             const float* ksum, const float* kmin, const float* kmax,
+                             float* kmean, int8_t* k_i8, float* k_scale, const SelArgs* sel,
+                             hipStream_t stream) {
   if (!k || !ksum || !kmin || !kmax || !kmean || !k_i8 || !k_scale) return RCSA_ERR_NULL;
+  // the fused launch exists for the layer call's shape only
+  if (sel && !(dtype == RCSA_BF16 && head_dim == 128 && block_size == 128 && n_blocks <= 1024))
+    return RCSA_ERR_SHAPE;
   if (slot_token && (src_len <= 0 || src_len >= (int64_t{1} << 31))) return RCSA_ERR_SHAPE;
   int st = check_pool_shape(dtype, batch, n_heads, n_blocks, block_size, head_dim,
                             stride_b, stride_h, stride_t);
@@ -641,7 +665,21 @@ extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
   PoolArgs a{k, n_heads, n_blocks, stride_b, stride_h, stride_t, valid, nullptr,
              const_cast<float*>(ksum), const_cast<float*>(kmin),
              const_cast<float*>(kmax), nullptr, nullptr, nullptr, slot_token, src_len};
-  dim3 grid(static_cast<unsigned>(nbh * n_blocks)), block(kPoolThreads);
+  dim3 block(kPoolThreads);
+  if (sel) {
+    const int64_t n_sel = (sel->n_rows + kSelWaves - 1) / kSelWaves;
+    dim3 grid(static_cast<unsigned>(n_sel + nbh * n_blocks));
+#define RCSA_QS(MAP, PER) \
+  quant_select_kernel<u16, 128, 128, MAP, PER><<<grid, block, 0, stream>>>(a, kmean, k_i8, k_scale, *sel, n_sel)
+    if (n_blocks <= 512) {
+      if (slot_token) RCSA_QS(true, 8); else RCSA_QS(false, 8);
+    } else {
+      if (slot_token) RCSA_QS(true, 16); else RCSA_QS(false, 16);
+    }
+#undef RCSA_QS
+    return launch_status();
+  }
+  dim3 grid(static_cast<unsigned>(nbh * n_blocks));
 #define RCSA_QK(T, D, BS)                                                                   \
   do {                                                                                      \
     if (slot_token) quant_key_kernel<T, D, BS, true><<<grid, block, 0, stream>>>(a, kmean, k_i8, k_scale); \
@@ -660,4 +698,39 @@ extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
   }
 #undef RCSA_QK
   return launch_status();
+}
+
+extern "C" int rcsa_quantize_key(const void* k, int dtype, int64_t batch,
+                                 int64_t n_heads, int64_t n_blocks, int64_t block_size,
+                                 int64_t head_dim, int64_t stride_b, int64_t stride_h,
+                                 int64_t stride_t, const uint8_t* valid,
+                                 const int32_t* slot_token, int64_t src_len,
+                                 const float* ksum, const float* kmin,
+                                 const float* kmax, float* kmean, int8_t* k_i8,
+                                 float* k_scale, hipStream_t stream) {
+  return quantize_key_impl(k, dtype, batch, n_heads, n_blocks, block_size, head_dim, stride_b,
+                           stride_h, stride_t, valid, slot_token, src_len, ksum, kmin, kmax,
+                           kmean, k_i8, k_scale, nullptr, stream);
+}
+
+extern "C" int rcsa_quantize_key_select(
+    const void* k, int dtype, int64_t batch, int64_t n_heads, int64_t n_blocks,
+    int64_t block_size, int64_t head_dim, int64_t stride_b, int64_t stride_h, int64_t stride_t,
+    const uint8_t* valid, const int32_t* slot_token, int64_t src_len, const float* ksum,
+    const float* kmin, const float* kmax, float* kmean, int8_t* k_i8, float* k_scale,
+    const float* qhat, const float* khat, int64_t n_qblocks, float* score,
+    const int32_t* row_k, int64_t row_k_stride_bh, int64_t k_fixed, const uint8_t* forced,
+    const uint8_t* allowed, int64_t mask_stride_bh, int32_t* indices, int64_t max_k,
+    int32_t* counts, hipStream_t stream) {
+  if (!qhat || !khat || !score || !indices || !counts) return RCSA_ERR_NULL;
+  if (n_qblocks <= 0 || max_k <= 0 || batch <= 0 || n_heads <= 0) return RCSA_ERR_SHAPE;
+  if (mask_stride_bh < 0 || row_k_stride_bh < 0) return RCSA_ERR_STRIDE;
+  if (!aligned16(qhat) || !aligned16(khat)) return RCSA_ERR_ALIGN;
+  if (head_dim != 128) return RCSA_ERR_SHAPE;  // the fused scores are unrolled for 128
+  const SelArgs sel{score, batch * n_heads * n_qblocks, n_qblocks, n_blocks, row_k,
+                    row_k_stride_bh, k_fixed, forced, allowed, mask_stride_bh, indices, max_k,
+                    counts, qhat, khat, head_dim};
+  return quantize_key_impl(k, dtype, batch, n_heads, n_blocks, block_size, head_dim, stride_b,
+                           stride_h, stride_t, valid, slot_token, src_len, ksum, kmin, kmax,
+                           kmean, k_i8, k_scale, &sel, stream);
 }

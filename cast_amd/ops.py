@@ -18,6 +18,7 @@ from ._lib import RCSA_BF16, RCSA_F32, RCSA_ORDER_INDEX, RCSA_ORDER_RANK, check
 __all__ = [
     "pool_query", "pool_key", "block_scores", "select_topk", "quantize_key",
     "sparse_attn_bf16", "sparse_attn_int8", "pack_tokens", "unpack_tokens", "row_budgets",
+    "quantize_key_select",
 ]
 
 
@@ -270,6 +271,21 @@ def select_topk(score: torch.Tensor, k, *, forced: Optional[torch.Tensor] = None
         raise TypeError(f"{fn}: score must be float32 [NBH, NQ, NK]")
     score = score.contiguous()
     nbh, nq, nk = score.shape
+    row_k, stride, k_fixed, max_k, fm, am, mstride = _selection_args(
+        nbh, nq, nk, k, forced, allowed, max_k, order, score.device, fn)
+    indices = torch.empty(nbh, nq, max_k, device=score.device, dtype=torch.int32)
+    counts = torch.empty(nbh, nq, device=score.device, dtype=torch.int32)
+    st = _lib.load().rcsa_select_topk(
+        score.data_ptr(), nbh, nq, nk, _ptr(row_k), stride, k_fixed, _ptr(fm), _ptr(am),
+        mstride, indices.data_ptr(), max_k, counts.data_ptr(),
+        RCSA_ORDER_RANK if order == "rank" else RCSA_ORDER_INDEX, _stream())
+    check(st, fn)
+    return indices, counts
+
+
+def _selection_args(nbh, nq, nk, k, forced, allowed, max_k, order, device, fn):
+    """(row_k, row_k stride, k_fixed, max_k, forced u8, allowed u8, mask stride) for the
+    selection ABI."""
     if isinstance(k, int):
         row_k, stride, k_fixed = None, 0, int(k)
         kmax = int(k)
@@ -285,28 +301,66 @@ def select_topk(score: torch.Tensor, k, *, forced: Optional[torch.Tensor] = None
             kmax = int(kt.max().item())  # host read of the budget; pass max_k to avoid it
         else:
             kmax = int(max_k)
-        row_k = kt.to(device=score.device, dtype=torch.int32).contiguous()
+        row_k = kt.to(device=device, dtype=torch.int32).contiguous()
         k_fixed = 0
     if max_k is None:
         max_k = max(1, min(kmax, nk))
     if order not in ("index", "rank"):
         raise ValueError(f"{fn}: order must be 'index' or 'rank'")
-    fm, fstride = _mask_u8(forced, nbh, nq, nk, score.device, fn)
-    am, astride = _mask_u8(allowed, nbh, nq, nk, score.device, fn)
+    fm, fstride = _mask_u8(forced, nbh, nq, nk, device, fn)
+    am, astride = _mask_u8(allowed, nbh, nq, nk, device, fn)
     if fm is not None and am is not None and fstride != astride:
         # the ABI shares one head stride between the masks: broadcast both
         fm = fm.expand(nbh, nq, nk).contiguous() if fstride == 0 else fm
         am = am.expand(nbh, nq, nk).contiguous() if astride == 0 else am
         fstride = astride = nq * nk
     mstride = fstride if fm is not None else astride
-    indices = torch.empty(nbh, nq, max_k, device=score.device, dtype=torch.int32)
-    counts = torch.empty(nbh, nq, device=score.device, dtype=torch.int32)
-    st = _lib.load().rcsa_select_topk(
-        score.data_ptr(), nbh, nq, nk, _ptr(row_k), stride, k_fixed, _ptr(fm), _ptr(am),
-        mstride, indices.data_ptr(), max_k, counts.data_ptr(),
-        RCSA_ORDER_RANK if order == "rank" else RCSA_ORDER_INDEX, _stream())
-    check(st, fn)
-    return indices, counts
+    return row_k, stride, k_fixed, max_k, fm, am, mstride
+
+
+def quantize_key_select(k, valid, block_size, ksum, kmin, kmax, qhat, khat, k_select, *,
+                        forced=None, allowed=None, max_k=None, slot_token=None):
+    """``quantize_key`` + ``block_scores`` + ``select_topk(order="index")`` with the key
+    quantiser and the selection in one launch (no reference counterpart: the int8 layer
+    call's form).  Returns ``(k_i8, k_scale, kmean, score, indices, counts)``, bit for bit
+    those of the separate calls.  Raises ``NotImplementedError`` for shapes the fused
+    launch does not cover (use the separate calls)."""
+    fn = "quantize_key_select"
+    _require_cuda(fn, k, ksum, kmin, kmax, qhat, khat)
+    code = _dtype_code(k, fn)
+    if slot_token is not None:
+        sm = _slot_map(slot_token, block_size, k.device, fn)
+        B, H, L, D, NB, src_len, strides = _tokens_bhld(k, sm, block_size, fn)
+    else:
+        sm, src_len = None, 0
+        B, H, L, D, NB = _bhld(k, block_size, fn)
+        strides = (k.stride(0), k.stride(1), k.stride(2))
+    if not (k.dtype == torch.bfloat16 and D == 128 and block_size == 128 and NB <= 1024):
+        raise NotImplementedError(f"{fn}: fused launch needs bf16 keys, D 128, 128-key "
+                                  "blocks and at most 1024 blocks")
+    for t in (ksum, kmin, kmax):
+        if t.shape != (B * H, NB, D) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{fn}: statistics must be contiguous float32 [{B * H}, {NB}, {D}]")
+    nbh, nq = B * H, qhat.shape[1]
+    for name, t, rows in (("qhat", qhat, nq), ("khat", khat, NB)):
+        if t.shape != (nbh, rows, D) or t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous float32 [{nbh}, {rows}, {D}]")
+    row_k, stride, k_fixed, max_k, fm, am, mstride = _selection_args(
+        nbh, nq, NB, k_select, forced, allowed, max_k, "index", k.device, fn)
+    v = _valid_u8(valid, L, k.device, fn)
+    kmean = torch.empty(nbh, D, device=k.device, dtype=torch.float32)
+    k_i8 = torch.empty(B, H, L, D, device=k.device, dtype=torch.int8)
+    k_scale = torch.empty(nbh, NB, device=k.device, dtype=torch.float32)
+    score = torch.empty(nbh, nq, NB, device=k.device, dtype=torch.float32)
+    indices = torch.empty(nbh, nq, max_k, device=k.device, dtype=torch.int32)
+    counts = torch.empty(nbh, nq, device=k.device, dtype=torch.int32)
+    check(_lib.load().rcsa_quantize_key_select(
+        k.data_ptr(), code, B, H, NB, block_size, D, *strides, _ptr(v), _ptr(sm), src_len,
+        ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(), k_i8.data_ptr(),
+        k_scale.data_ptr(), qhat.data_ptr(), khat.data_ptr(), nq, score.data_ptr(),
+        _ptr(row_k), stride, k_fixed, _ptr(fm), _ptr(am), mstride, indices.data_ptr(), max_k,
+        counts.data_ptr(), _stream()), fn)
+    return k_i8, k_scale, kmean, score, indices, counts
 
 
 def quantize_key(k: torch.Tensor, valid: Optional[torch.Tensor], block_size: int,

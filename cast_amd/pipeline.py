@@ -59,7 +59,8 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                    return_lse: bool = False, order: str = "index",
                    n_split: Optional[int] = None, overlap: bool = True,
                    q_slot_token: Optional[torch.Tensor] = None,
-                   k_slot_token: Optional[torch.Tensor] = None) -> RCSAResult:
+                   k_slot_token: Optional[torch.Tensor] = None,
+                   fuse_select: bool = True) -> RCSAResult:
     """One RCSA layer call over packed Q/K/V ``[B, H, NB*BS, D]`` (bf16 or fp32).
 
     ``k_select`` is the per-row number of key blocks handed to attention
@@ -68,8 +69,10 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     With ``int8`` QK^T runs on int8 MFMA over smoothed per-block quantised
     Q/K; otherwise on bf16 MFMA.  ``n_split`` splits every block list over
     that many workgroups (None: chosen from the device's compute-unit count).
+    ``fuse_select`` (int8, index order, bf16 keys of D 128 in 128-key blocks)
+    scores and selects inside the key quantiser's launch; otherwise
     ``overlap`` runs the scores and the top-k on a side stream beside the
-    int8 key pass (int8 only; results are identical either way).
+    int8 key pass.  Results are identical either way.
 
     ``q_slot_token`` / ``k_slot_token`` (int8 only, both or neither; e.g. a
     ``CompactLayout.slot_token``): q, k and v are token-major ``[B, L, H, D]``
@@ -109,29 +112,38 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs)
         khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs)
         k_mask = None
-    if side is not None:
-        side.wait_stream(main)  # qhat and khat
+    # int8 at the layer call's shape: the scores and the top-k run inside the
+    # key quantiser's launch (one stream, no cross-stream waits)
+    fused = (int8 and fuse_select and order == "index" and k.dtype == torch.bfloat16
+             and D == 128 and bs == 128 and Lk // bs <= 1024)
+    if fused:
+        k_i8, k_scale, kmean, score, indices, counts = ops.quantize_key_select(
+            k, k_valid, bs, ksum, kmin, kmax, qhat, khat, k_select, forced=forced,
+            allowed=allowed, max_k=max_k, slot_token=k_slot_token)
+    else:
+        if side is not None:
+            side.wait_stream(main)  # qhat and khat
 
-    def score_and_select():
-        sc = ops.block_scores(qhat, khat)
-        return sc, ops.select_topk(sc, k_select, forced=forced, allowed=allowed,
-                                   max_k=max_k, order=order)
+        def score_and_select():
+            sc = ops.block_scores(qhat, khat)
+            return sc, ops.select_topk(sc, k_select, forced=forced, allowed=allowed,
+                                       max_k=max_k, order=order)
 
-    score, (indices, counts) = on_side(score_and_select)
+        score, (indices, counts) = on_side(score_and_select)
+        if int8:
+            k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax,
+                                                    slot_token=k_slot_token)
+        if side is not None:
+            main.wait_stream(side)  # the selection
+            # No record_stream: the side stream is private to this function and
+            # every use of it starts after a wait on the caller's stream, so memory
+            # freed on either stream is reused only after the other stream's use.
+            # (Each recorded stream would add event packets between the kernels.)
     nqb = Lq // bs
     idx4 = indices.view(B, H, nqb, -1)
     cnt3 = counts.view(B, H, nqb)
     scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
     lse = None
-    if int8:
-        k_i8, k_scale, kmean = ops.quantize_key(k, k_valid, bs, ksum, kmin, kmax,
-                                                slot_token=k_slot_token)
-    if side is not None:
-        main.wait_stream(side)  # the selection
-        # No record_stream: the side stream is private to this function and
-        # every use of it starts after a wait on the caller's stream, so memory
-        # freed on either stream is reused only after the other stream's use.
-        # (Each recorded stream would add event packets between the kernels.)
     if int8:
         res = ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v if v.dtype == torch.bfloat16
                                    else v.to(torch.bfloat16), idx4, cnt3, None,

@@ -193,6 +193,31 @@ int rcsa_quantize_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
                       int8_t* k_i8, float* k_scale, hipStream_t stream);
 
 /*
+ * rcsa_quantize_key, rcsa_block_scores and rcsa_select_topk (index order) in
+ * two launches instead of four: the key mean, then one launch whose first
+ * workgroups score and select the rows (one wavefront per row) while the rest
+ * quantise the key tiles.  Outputs are those of the separate calls bit for
+ * bit (each score is summed over the channels in rcsa_block_scores' order).
+ * No reference counterpart: the int8 layer call's form, replacing a side
+ * stream and its two cross-stream waits.  qhat [n_bh][n_qblocks][D] and khat
+ * [n_bh][n_blocks][D] come from the pooling pass; score receives
+ * [n_bh][n_qblocks][n_blocks]; the selection arguments are those of
+ * rcsa_select_topk.  bf16 keys, head_dim 128, block_size 128 and n_blocks <=
+ * 1024 only (RCSA_ERR_SHAPE otherwise: use the separate calls).
+ */
+int rcsa_quantize_key_select(const void* k, int dtype, int64_t batch, int64_t n_heads,
+                             int64_t n_blocks, int64_t block_size, int64_t head_dim,
+                             int64_t stride_b, int64_t stride_h, int64_t stride_t,
+                             const uint8_t* valid, const int32_t* slot_token, int64_t src_len,
+                             const float* ksum, const float* kmin, const float* kmax,
+                             float* kmean, int8_t* k_i8, float* k_scale, const float* qhat,
+                             const float* khat, int64_t n_qblocks, float* score,
+                             const int32_t* row_k, int64_t row_k_stride_bh, int64_t k_fixed,
+                             const uint8_t* forced, const uint8_t* allowed,
+                             int64_t mask_stride_bh, int32_t* indices, int64_t max_k,
+                             int32_t* counts, hipStream_t stream);
+
+/*
  * Block-sparse flash attention, bf16 Q/K/V, fp32 online softmax.
  * Drop-in for wan.modules.longcat_kernel._attn_fwd_bsa_align as launched by
  * _longcat_active (P/matrix_jit_spatial_acceleration.py:663-729) and
