@@ -132,16 +132,19 @@ def test_c2_int8_layer(dev):
 
 
 def test_c2_side_stream_matches_serial(dev):
-    """The query side on its own stream gives the serial call's results bit
-    for bit, over several back-to-back calls without host syncs between."""
+    """The scores and top-k on their own stream (the unfused form) give the
+    serial call's results bit for bit, over several back-to-back calls without
+    host syncs between; so does the fused launch."""
     from cast_amd import workloads
     from cast_amd.pipeline import rcsa_attention
     g = workloads.matrix_dit(2, heads=4, int8=True).to(dev)
     kw = dict(block_size=128, k_select=g.k_total, forced=g.forced, int8=True,
               return_lse=True)
-    ref = rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, overlap=False, **kw)
-    runs = [rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, overlap=True, **kw)
-            for _ in range(3)]
+    ref = rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, overlap=False,
+                         fuse_select=False, **kw)
+    runs = [rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, overlap=True,
+                           fuse_select=False, **kw) for _ in range(3)]
+    runs.append(rcsa_attention(g.q, g.k, g.v, g.q_valid, g.k_valid, **kw))
     torch.cuda.synchronize()
     for i, res in enumerate(runs):
         for name in ("out", "lse", "indices", "counts", "score", "q_i8", "q_scale", "k_i8",
