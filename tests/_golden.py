@@ -39,7 +39,18 @@ def workload(name: str):
         return workloads.matrix_dit(0, int8=True)
     if name == "c3_selection":
         return workloads.selection_stress(0)
+    if name.startswith(("c1_seed", "c2_seed")):  # c1_seed3, c2_seed1, ...
+        return workloads.matrix_dit(int(name[len("c1_seed"):]), int8=name.startswith("c2"))
     raise KeyError(name)
+
+
+def seed_fixture(name: str) -> dict:
+    """The per-seed slice of c1_seeds.npz / c2_seeds.npz as a plain dict
+    (``c1_seed3`` -> the ``s3_*`` arrays without their prefix)."""
+    seed = int(name[len("c1_seed"):])
+    fx = load(f"{name[:2]}_seeds")
+    pre = f"s{seed}_"
+    return {k[len(pre):]: v for k, v in fx.items() if k.startswith(pre)}
 
 
 def set_equal_where(idx_a, cnt_a, idx_b, cnt_b, rows_mask) -> int:

@@ -15,6 +15,9 @@ tests/test_oracle_pins.py) on the seeded synthetic workloads of
                        int8 attention rows of head 0, query blocks 0 and 27
   c3_selection.npz     C3 (825 history blocks, k=64 with 8 forced, 10% near
                        ties): selection + margins of every row
+  c1_seeds.npz         C1 at seeds 1-4: selection + margins of every row, fp32
+  c2_seeds.npz         attention rows of one head (5 * seed mod 24) for query
+                       blocks 0 and 27 (C2: the unquantised fp32 rows)
 
 Run from the repository root: ``python tests/golden/make_golden.py``.
 """
@@ -140,13 +143,52 @@ def make_c3() -> dict:
     }
 
 
+SEEDS = (1, 2, 3, 4)
+
+
+def seed_head(seed: int) -> int:
+    return (5 * seed) % 24
+
+
+def make_seeds(int8: bool) -> dict:
+    """Selection of every row and fp32 attention rows of one head, per seed."""
+    out = {}
+    for seed in SEEDS:
+        w = workloads.matrix_dit(seed, int8=int8)
+        score = _scores(w)
+        idx, cnt, margin = _selection(w, score)
+        B, H = w.q.shape[:2]
+        nqb, bs, h = w.n_qblocks, w.block_size, seed_head(seed)
+        o, lse = orc.sparse_attention(w.q, w.k, w.v, idx.reshape(B, H, nqb, -1),
+                                      cnt.reshape(B, H, nqb), w.k_valid, block_m=bs,
+                                      block_n=bs, heads=[h], qblocks=list(ATTN_QBLOCKS))
+        rows = torch.cat([torch.arange(m * bs, (m + 1) * bs) for m in ATTN_QBLOCKS])
+        out[f"s{seed}_fingerprint"] = np.array(workload_fingerprint(w))
+        out[f"s{seed}_indices"] = idx.numpy().astype(np.int16)
+        out[f"s{seed}_counts"] = cnt.numpy()
+        out[f"s{seed}_margin"] = margin.numpy()
+        out[f"s{seed}_head"] = np.array(h)
+        out[f"s{seed}_attn_rows"] = rows.numpy()
+        out[f"s{seed}_out"] = o[0, h, rows].numpy()
+        out[f"s{seed}_lse"] = lse[0, h, rows].numpy()
+        print(f"seed {seed} int8={int8} done", flush=True)
+    return out
+
+
 def main() -> None:
+    if sys.argv[1:] == ["seeds"]:  # only the multi-seed fixtures
+        torch.set_num_threads(min(8, os.cpu_count() or 1))
+        np.savez_compressed(os.path.join(HERE, "c1_seeds.npz"), **make_seeds(False))
+        np.savez_compressed(os.path.join(HERE, "c2_seeds.npz"), **make_seeds(True))
+        return
     torch.set_num_threads(min(8, os.cpu_count() or 1))
     np.savez_compressed(os.path.join(HERE, "c0_plumbing.npz"), **make_c0())
     c1, c2 = make_c1_c2()
     np.savez_compressed(os.path.join(HERE, "c1_dit_bf16.npz"), **c1)
     np.savez_compressed(os.path.join(HERE, "c2_dit_int8.npz"), **c2)
     np.savez_compressed(os.path.join(HERE, "c3_selection.npz"), **make_c3())
+    np.savez_compressed(os.path.join(HERE, "c1_seeds.npz"), **make_seeds(False))
+    np.savez_compressed(os.path.join(HERE, "c2_seeds.npz"), **make_seeds(True))
     for name in sorted(os.listdir(HERE)):
         if name.endswith(".npz"):
             print(f"{name}: {os.path.getsize(os.path.join(HERE, name))} bytes")

@@ -14,6 +14,24 @@ def test_generator_fingerprint(name):
     assert _golden.fingerprint(_golden.workload(name)) == str(fx["fingerprint"])
 
 
+@pytest.mark.parametrize("name", [f"c{c}_seed{s}" for c in (1, 2) for s in (1, 2, 3, 4)])
+def test_seed_fixture(name):
+    """Seeds 1-4: the generator still makes the fixture's inputs, every row
+    keeps the forced current blocks and the full budget, and the oracle
+    reproduces the selection of one head."""
+    fx = _golden.seed_fixture(name)
+    w = _golden.workload(name)
+    assert _golden.fingerprint(w) == str(fx["fingerprint"])
+    idx, cnt = fx["indices"], fx["counts"]
+    assert np.all(cnt == w.k_total)
+    cur = set(range(w.n_hist_blocks, w.n_kblocks))
+    assert all(cur <= set(idx[r, i, :cnt[r, i]].tolist())
+               for r in range(idx.shape[0]) for i in range(idx.shape[1]))
+    h = int(fx["head"])
+    i0, _ = orc.select_topk(_scores(w, [h]), w.k_total, forced=w.forced)
+    np.testing.assert_array_equal(i0.numpy(), idx[h:h + 1])
+
+
 def test_c0_oracle_reproduces_fixture():
     fx = _golden.load("c0_plumbing")
     w = _golden.workload("c0_plumbing")
