@@ -42,6 +42,9 @@ SIGNATURES: dict[str, list] = {
                                    + [_I] * 8 + [_I, _P, _I, _P],
     "rcsa_sparse_attn_int8_split": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P, _P]
                                    + [_I] * 18 + [_I] * 8 + [_I, _P, _I, _P, _I, _P],
+    "rcsa_sparse_attn_int8_noalloc": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P,
+                                      _P] + [_I] * 18 + [_I] * 8 + [_I, _P, _I, _P],
+    "rcsa_attn_noalloc_scratch_bytes": [],
     "rcsa_attn_workspace_bytes": [_I, _I, _I, _I, _I],
     "rcsa_attn_split_plan": [_I, _I, _I, _I, _I, ctypes.POINTER(c_int64)],
     "rcsa_pack_tokens": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
@@ -68,7 +71,9 @@ def load() -> ctypes.CDLL:
         fn = getattr(lib, name)
         fn.argtypes = argtypes
         fn.restype = (ctypes.c_char_p if name == "rcsa_status_string"
-                      else c_int64 if name == "rcsa_attn_workspace_bytes" else c_int)
+                      else c_int64 if name in ("rcsa_attn_workspace_bytes",
+                                               "rcsa_attn_noalloc_scratch_bytes")
+                      else c_int)
     _lib = lib
     return lib
 

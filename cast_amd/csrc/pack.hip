@@ -115,6 +115,7 @@ extern "C" const char* rcsa_status_string(int status) {
     case RCSA_ERR_DTYPE: return "unsupported dtype code";
     case RCSA_ERR_LAUNCH: return "HIP launch failed";
     case RCSA_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case RCSA_ERR_SCRATCH: return "split workspace exceeds the library's static scratch";
     default: return "unknown status";
   }
 }

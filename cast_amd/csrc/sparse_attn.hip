@@ -29,6 +29,7 @@
 // running max is only moved when a row's max grows by more than 2^8
 // (rescaling O is skipped otherwise).  Row sums accumulate the fp32
 // probabilities (P is rounded to bf16 only as the PV operand).
+#include <mutex>
 #include <type_traits>
 
 #include "rcsa_common.h"
@@ -900,14 +901,11 @@ static int64_t ws_bound(int64_t n_bh, int64_t q_len, int64_t d, int64_t n_split)
 }
 
 // Tail query blocks: on each XCD, those past the last full round of its
-// compute units (all of them when one round is not filled).
-static int apply_split(AttnArgs& a, int64_t d, int64_t n_split, void* workspace,
-                       int64_t workspace_bytes) {
+// compute units (all of them when one round is not filled).  Sets the split
+// fields of `a` (no workspace yet); leaves `a` unsplit when every round is full.
+static int plan_split(AttnArgs& a, int64_t n_split) {
   if (n_split < 1 || n_split > 16) return RCSA_ERR_SHAPE;
   if (n_split == 1) return RCSA_OK;
-  if (workspace == nullptr) return RCSA_ERR_NULL;
-  if (!aligned16(workspace)) return RCSA_ERR_ALIGN;
-  if (workspace_bytes < ws_bound(a.n_bh, a.q_len, d, n_split)) return RCSA_ERR_SHAPE;
   const int64_t cux = cus_per_xcd();
   if (cux <= 0) return RCSA_ERR_LAUNCH;
   const int64_t p = a.xcd_items;
@@ -916,9 +914,59 @@ static int apply_split(AttnArgs& a, int64_t d, int64_t n_split, void* workspace,
   a.xcd_direct = direct;
   a.n_split = n_split;
   a.n_tail = kNumXcd * (p - direct);
-  a.ws_o = static_cast<u16*>(workspace);
-  a.ws_ml = reinterpret_cast<float2*>(static_cast<char*>(workspace) +
-                                      ws_o_bytes(a.n_tail, a.block_m, d, n_split));
+  return RCSA_OK;
+}
+
+// Bytes of workspace a planned split launch uses (0 when unsplit).
+static int64_t split_need(const AttnArgs& a, int64_t d) {
+  if (a.n_split == 1) return 0;
+  return ws_o_bytes(a.n_tail, a.block_m, d, a.n_split) + a.n_split * a.n_tail * a.block_m * 8;
+}
+
+// Point the partial outputs and (max, sum) pairs of a planned split at `base`.
+static void bind_workspace(AttnArgs& a, int64_t d, char* base) {
+  a.ws_o = reinterpret_cast<u16*>(base);
+  a.ws_ml = reinterpret_cast<float2*>(base + ws_o_bytes(a.n_tail, a.block_m, d, a.n_split));
+}
+
+static int apply_split(AttnArgs& a, int64_t d, int64_t n_split, void* workspace,
+                       int64_t workspace_bytes) {
+  if (n_split < 1 || n_split > 16) return RCSA_ERR_SHAPE;
+  if (n_split == 1) return RCSA_OK;
+  if (workspace == nullptr) return RCSA_ERR_NULL;
+  if (!aligned16(workspace)) return RCSA_ERR_ALIGN;
+  if (workspace_bytes < ws_bound(a.n_bh, a.q_len, d, n_split)) return RCSA_ERR_SHAPE;
+  const int st = plan_split(a, n_split);
+  if (st || a.n_split == 1) return st;
+  bind_workspace(a, d, static_cast<char*>(workspace));
+  return RCSA_OK;
+}
+
+// ---- the allocation-free entry point's scratch ----
+// Device-resident workspace of rcsa_sparse_attn_int8_noalloc: the split
+// shares' partial outputs and (max, sum) pairs.  Every GPU the library runs on
+// holds its own copy until the process ends.  Host code must not use the
+// array's name as an address (it is a host-side stand-in): the device address
+// comes from hipGetSymbolAddress, once per device, in scratch_on_device().
+constexpr int64_t kScratchBytes = int64_t{32} << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::mutex g_scratch_mu;
+static char* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's address of `scratch` (looked up on the first call per device).
+static int scratch_on_device(char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return RCSA_ERR_LAUNCH;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr)
+      return RCSA_ERR_LAUNCH;
+    g_scratch_ptr[dev] = static_cast<char*>(p);
+  }
+  *out = g_scratch_ptr[dev];
   return RCSA_OK;
 }
 
@@ -1056,6 +1104,66 @@ extern "C" int rcsa_sparse_attn_int8_split(
   if (a.n_items == 0) return RCSA_OK;
   return launch_attn_split<true>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
 }
+
+// The split int8 entry point with the library's static scratch as its
+// workspace: allocates nothing.  Planned exactly like the split entry point;
+// a split needing more than kScratchBytes is refused with RCSA_ERR_SCRATCH.
+extern "C" int rcsa_sparse_attn_int8_noalloc(
+    const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
+    const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
+    const uint32_t* K_block_mask, float sm_scale, float* M, void* Out,
+    const int32_t* block_indices,
+    const int32_t* block_indices_lens, int64_t stride_qz, int64_t stride_qh,
+    int64_t stride_qm, int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+    int64_t stride_vz, int64_t stride_vh, int64_t stride_vn, int64_t stride_oz,
+    int64_t stride_oh, int64_t stride_om, int64_t stride_bz, int64_t stride_bh,
+    int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
+    int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
+    int64_t BLOCK_N, int64_t max_k, int64_t n_split, const int32_t* out_token,
+    int64_t out_len, hipStream_t stream) {
+  if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
+  AttnArgs a{};
+  a.q = Q;
+  a.k = K;
+  a.v = static_cast<const u16*>(V);
+  a.q_scale = q_scale;
+  a.k_scale = k_scale;
+  a.q_scale_stride = q_scale_stride;
+  a.k_scale_stride = k_scale_stride;
+  int st = fill_common(a, K_valid, sm_scale, M, Out, block_indices, block_indices_lens,
+                       stride_qz, stride_qh, stride_qm, stride_kz, stride_kh, stride_kn,
+                       stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
+                       stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B,
+                       H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 16);
+  if (st) return st;
+  if (q_scale_stride < a.n_qblocks || k_scale_stride < a.n_kblocks) return RCSA_ERR_STRIDE;
+  if (out_token) {
+    if (out_len <= 0 || out_len >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
+    a.out_tok = out_token;
+    a.out_len = out_len;
+  }
+  if (K_block_mask) {
+    if (reinterpret_cast<uintptr_t>(K_block_mask) & 3u) return RCSA_ERR_ALIGN;
+    a.kmask = K_block_mask;
+    a.kvalid = nullptr;
+  }
+  st = plan_split(a, n_split);
+  if (st) return st;
+  if (split_need(a, HEAD_DIM) > kScratchBytes) return RCSA_ERR_SCRATCH;
+  if (a.n_split > 1) {
+    // every share writes all its rows' partials and (max, sum) before the
+    // merge reads them, so nothing left from an earlier call is read
+    char* base = nullptr;
+    st = scratch_on_device(&base);
+    if (st) return st;
+    bind_workspace(a, HEAD_DIM, base);
+  }
+  if (a.n_items == 0) return RCSA_OK;
+  return launch_attn_split<true>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
+}
+
+extern "C" int64_t rcsa_attn_noalloc_scratch_bytes(void) { return kScratchBytes; }
 
 extern "C" int rcsa_sparse_attn_bf16(
     const void* Q, const void* K, const void* V, const uint8_t* K_valid, float sm_scale,

@@ -35,7 +35,8 @@ enum {
   RCSA_ERR_STRIDE = 3,   /* last dimension not contiguous / misaligned stride */
   RCSA_ERR_DTYPE = 4,    /* unsupported element type code */
   RCSA_ERR_LAUNCH = 5,   /* the HIP runtime rejected the launch */
-  RCSA_ERR_ALIGN = 6     /* a pointer is not 16-byte aligned */
+  RCSA_ERR_ALIGN = 6,    /* a pointer is not 16-byte aligned */
+  RCSA_ERR_SCRATCH = 7   /* the request exceeds the library's static scratch */
 };
 
 /* Element type codes for inputs that may be bf16 or fp32. */
@@ -332,6 +333,40 @@ int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t max_k, int64_t n_split, void* workspace,
                                 int64_t workspace_bytes, const int32_t* out_token,
                                 int64_t out_len, hipStream_t stream);
+
+/*
+ * The split int8 entry point with no workspace argument: it allocates
+ * nothing.  No reference counterpart; it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  The split shares' partial outputs and (max, sum)
+ * pairs live in a static device array of rcsa_attn_noalloc_scratch_bytes()
+ * bytes (32 MiB) that each GPU holds until the process ends; a split whose
+ * workspace would exceed it returns RCSA_ERR_SCRATCH (n_split 3 covers up to
+ * 8 * 31 = 248 tail query blocks of 128 rows at HEAD_DIM 128).  Every call on
+ * one GPU shares that GPU's array: calls that overlap on one GPU (different
+ * streams, or threads) race.  Arguments and results as
+ * rcsa_sparse_attn_int8_split.
+ */
+int rcsa_sparse_attn_int8_noalloc(const int8_t* Q, const float* q_scale,
+                                  int64_t q_scale_stride, const int8_t* K,
+                                  const float* k_scale, int64_t k_scale_stride,
+                                  const void* V, const uint8_t* K_valid,
+                                  const uint32_t* K_block_mask, float sm_scale,
+                                  float* M, void* Out, const int32_t* block_indices,
+                                  const int32_t* block_indices_lens,
+                                  int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,
+                                  int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+                                  int64_t stride_vz, int64_t stride_vh, int64_t stride_vn,
+                                  int64_t stride_oz, int64_t stride_oh, int64_t stride_om,
+                                  int64_t stride_bz, int64_t stride_bh, int64_t stride_bm,
+                                  int64_t stride_lz, int64_t stride_lh, int64_t stride_lm,
+                                  int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
+                                  int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
+                                  int64_t max_k, int64_t n_split, const int32_t* out_token,
+                                  int64_t out_len, hipStream_t stream);
+
+/* Size in bytes of the static scratch of rcsa_sparse_attn_int8_noalloc. */
+int64_t rcsa_attn_noalloc_scratch_bytes(void);
 
 /* Workspace bytes of a split launch on the current device, an upper bound
  * for BLOCK_M in {64, 128} (0 for n_split == 1, -1 on bad sizes). */
