@@ -66,6 +66,10 @@ def load() -> ctypes.CDLL:
             f"RCSA HIP library not built: {LIB_PATH} is missing "
             "(run `python -m cast_amd.build`)"
         )
+    # torch first: the library must bind to the HIP runtime torch already loaded
+    # (loaded first, the library would bring in a second runtime whose kernels
+    # cannot run on torch's streams)
+    import torch  # noqa: F401
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, argtypes in SIGNATURES.items():
         fn = getattr(lib, name)
