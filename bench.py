@@ -211,7 +211,8 @@ def main() -> int:
                                               block_n=bs, out=out, block_mask=r.k_mask)
         else:
             fn = lambda: ops.sparse_attn_bf16(w.q, w.k, w.v, r.indices, r.counts,  # noqa
-                                              w.k_valid, block_m=bs, block_n=bs, out=out)
+                                              None, block_m=bs, block_n=bs, out=out,
+                                              block_mask=r.k_mask)
         torch.cuda.synchronize()
         ms = _events_time(fn, args.steps, args.warmup)
         ops_attn = w.attention_ops(r.indices, r.counts)
@@ -333,11 +334,16 @@ def main() -> int:
                             k_select=wb.k_total, forced=wb.forced, int8=False, max_k=max_k)
         outb = torch.empty_like(wb.q)
         bf_ms = _events_time(lambda: ops.sparse_attn_bf16(
+            wb.q, wb.k, wb.v, rb.indices, rb.counts, None, block_m=bs, block_n=bs,
+            out=outb, block_mask=rb.k_mask), iters)
+        bf_bytes_ms = _events_time(lambda: ops.sparse_attn_bf16(
             wb.q, wb.k, wb.v, rb.indices, rb.counts, wb.k_valid, block_m=bs, block_n=bs,
             out=outb), iters)
         bf_ops = wb.attention_ops(rb.indices, rb.counts)
         extras["bf16_attn"] = {"ms": bf_ms, "TFLOP/s": bf_ops / bf_ms / 1e9,
-                               "frac_bf16_peak": bf_ops / bf_ms / 1e9 / BF16_PEAK_TFLOPS}
+                               "frac_bf16_peak": bf_ops / bf_ms / 1e9 / BF16_PEAK_TFLOPS,
+                               "validity": "bits (key pooling pass)",
+                               "ms_validity_bytes": bf_bytes_ms}
         del wb, rb, outb
         # per-denoising-step sweep: 30 layers, 1-4 anchor frames, 12.5-50% budget
         plan = workloads.step_sweep_plan(args.seed)

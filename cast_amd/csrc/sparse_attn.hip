@@ -179,7 +179,10 @@ struct AttnCfg {
   static constexpr int V_RPU = 1024 / VROW;
   static constexpr int MW = NDT * 16 * 64 + 128; // floats of one row group's merge partial
   static constexpr int MPER = (NRG + STAGES - 1) / STAGES;  // partials per slot
-  static constexpr bool MERGE_IN_SLOTS = MPER * MW * 4 <= BUF;
+  // a 3-slot ring's slots are grown to hold the key-half merge partials (the
+  // 64-key bf16 ring: 2 x 16.5 KiB in each 32.25 KiB slot)
+  static constexpr int SLOT = (STAGES == 3 && MPER * MW * 4 > BUF + 256) ? MPER * MW * 4 : BUF + 256;
+  static constexpr bool MERGE_IN_SLOTS = MPER * MW * 4 <= SLOT;
   // the vmcnt accounting of a 3-deep ring needs the same copy count on every wavefront
   static_assert(STAGES == 2 || (KUNITS % NW == 0 && VUNITS % NW == 0), "uneven copies");
   static_assert(QSTEPS * 2 == CPR_K, "K chunk layout");
@@ -204,18 +207,24 @@ __device__ __forceinline__ void buffer_copy4(char* base, int bytes, uint32_t vof
 }
 
 // Waves per SIMD the register budget is sized for.  A ring of BNS < BN keys
-// fits two workgroups in one compute unit's LDS, so exactly two waves of
-// each SIMD's share must fit; otherwise the compiler's default range applies
-// (at least the workgroup's own waves per SIMD).
-template <int BN, int BNS, int NKH, int NT>
-constexpr int attn_waves_min() { return BNS < BN ? 2 * NKH : (NT / 256 > 1 ? NT / 256 : 1); }
-template <int BN, int BNS, int NKH>
-constexpr int attn_waves_max() { return BNS < BN ? 2 * NKH : 8; }
+// whose slots hold at most 80 KiB fits two workgroups in one compute unit's
+// LDS, so exactly two waves of each SIMD's share must fit; otherwise the
+// compiler's default range applies (at least the workgroup's own waves per SIMD).
+template <bool INT8, int D, int BN, int STAGES, int BNS>
+constexpr bool attn_two_wg() {
+  return BNS < BN && STAGES * BNS * (D * (INT8 ? 1 : 2) + 2 * D) <= 80 * 1024;
+}
+template <bool INT8, int D, int BN, int STAGES, int BNS, int NKH, int NT>
+constexpr int attn_waves_min() {
+  return attn_two_wg<INT8, D, BN, STAGES, BNS>() ? 2 * NKH : (NT / 256 > 1 ? NT / 256 : 1);
+}
+template <bool INT8, int D, int BN, int STAGES, int BNS, int NKH>
+constexpr int attn_waves_max() { return attn_two_wg<INT8, D, BN, STAGES, BNS>() ? 2 * NKH : 8; }
 
 template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH, bool MASK>
 __global__ void __launch_bounds__(BM * 2 * NKH)  // == AttnCfg::NT
-__attribute__((amdgpu_waves_per_eu(attn_waves_min<BN, BNS, NKH, BM * 2 * NKH>(),
-                                   attn_waves_max<BN, BNS, NKH>())))
+__attribute__((amdgpu_waves_per_eu(attn_waves_min<INT8, D, BN, STAGES, BNS, NKH, BM * 2 * NKH>(),
+                                   attn_waves_max<INT8, D, BN, STAGES, BNS, NKH>())))
 sparse_attn_kernel(AttnArgs a) {
   using C = AttnCfg<INT8, D, BM, BN, STAGES, BNS, NKH>;
   typedef typename std::conditional<INT8, v4i, v8bf>::type OpT;
@@ -230,9 +239,9 @@ sparse_attn_kernel(AttnArgs a) {
   // Ring slots are separate arrays and the loop is unrolled over them, so
   // the compiler can prove that reads of slot j do not alias the copies in
   // flight into the other slots (it would otherwise drain them first).
-  __shared__ __attribute__((aligned(1024))) char s_0[C::BUF + 256];
-  __shared__ __attribute__((aligned(1024))) char s_1[C::BUF + 256];
-  __shared__ __attribute__((aligned(1024))) char s_2[STAGES > 2 ? C::BUF + 256 : 16];
+  __shared__ __attribute__((aligned(1024))) char s_0[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) char s_1[C::SLOT];
+  __shared__ __attribute__((aligned(1024))) char s_2[STAGES > 2 ? C::SLOT : 16];
   __shared__ __attribute__((aligned(16)))
   char s_m[NKH == 1 || C::MERGE_IN_SLOTS ? 16 : C::NRG * C::MW * 4];
 
@@ -849,6 +858,15 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
       return launch_status();
     }
   }
+  if constexpr (!INT8) {  // bf16 at D 128: a 3-slot ring of 64-key steps (3 x 32 KiB)
+    if (D == 128 && BM == 128 && BN == 128) {
+      if (a.kmask != nullptr)
+        sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, true><<<grid, dim3(512), 0, s>>>(a);
+      else
+        sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, false><<<grid, dim3(512), 0, s>>>(a);
+      return launch_status();
+    }
+  }
   RCSA_ATTN(128, 128, 128, INT8 ? 3 : 2)
   RCSA_ATTN(128, 128, 64, 2)
   RCSA_ATTN(128, 64, 128, 2)
@@ -1032,7 +1050,8 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
 using namespace rcsa;
 
 extern "C" int rcsa_sparse_attn_bf16_split(
-    const void* Q, const void* K, const void* V, const uint8_t* K_valid, float sm_scale,
+    const void* Q, const void* K, const void* V, const uint8_t* K_valid,
+    const uint32_t* K_block_mask, float sm_scale,
     float* M, void* Out, const int32_t* block_indices, const int32_t* block_indices_lens,
     int64_t stride_qz, int64_t stride_qh, int64_t stride_qm, int64_t stride_kz,
     int64_t stride_kh, int64_t stride_kn, int64_t stride_vz, int64_t stride_vh,
@@ -1053,6 +1072,11 @@ extern "C" int rcsa_sparse_attn_bf16_split(
                        stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B,
                        H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 8);
   if (st) return st;
+  if (K_block_mask) {  // the bits replace the validity bytes
+    if (reinterpret_cast<uintptr_t>(K_block_mask) & 3u) return RCSA_ERR_ALIGN;
+    a.kmask = K_block_mask;
+    a.kvalid = nullptr;
+  }
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
   if (a.n_items == 0) return RCSA_OK;
@@ -1176,7 +1200,7 @@ extern "C" int rcsa_sparse_attn_bf16(
     int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N, int64_t max_k,
     hipStream_t stream) {
   return rcsa_sparse_attn_bf16_split(
-      Q, K, V, K_valid, sm_scale, M, Out, block_indices, block_indices_lens, stride_qz,
+      Q, K, V, K_valid, nullptr, sm_scale, M, Out, block_indices, block_indices_lens, stride_qz,
       stride_qh, stride_qm, stride_kz, stride_kh, stride_kn, stride_vz, stride_vh, stride_vn,
       stride_oz, stride_oh, stride_om, stride_bz, stride_bh, stride_bm, stride_lz, stride_lh,
       stride_lm, B, H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, stream);

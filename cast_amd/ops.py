@@ -435,12 +435,26 @@ def _expand_lists(indices, counts, B, H):
     return indices.expand(B, H, -1, -1), counts.expand(B, H, -1)
 
 
+def _check_block_mask(block_mask, Lk, block_n, device, fn):
+    """The key-validity bits as the kernels read them: int32 [ceil(Lk / block_n),
+    block_n // 32], contiguous, on ``device``."""
+    nkb = -(-Lk // block_n)
+    if block_mask.dtype != torch.int32 or block_mask.device != device \
+            or block_mask.numel() < nkb * (block_n // 32):
+        raise ValueError(f"{fn}: block_mask must be int32 [{nkb}, {block_n // 32}] "
+                         "on the same device")
+    return block_mask.contiguous()
+
+
 def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block_n=128,
-                     sm_scale=None, return_lse=False, out=None, n_split=None):
+                     sm_scale=None, return_lse=False, out=None, n_split=None,
+                     block_mask=None):
     """bf16 block-sparse attention; the ``_attn_fwd_bsa_align`` contract.
 
     q/k/v [B, H, L, D] bf16, indices int32 [B|1, H|1, NQB, maxK], counts
     int32 [B|1, H|1, NQB], valid: per key token (K_LEN entries) or None.
+    ``block_mask`` (the key validity as bits, as :func:`pool_key` writes it)
+    replaces ``valid`` when given.
     ``n_split`` splits every block list over that many workgroups (merged
     afterwards); None picks it from the device's compute-unit count.
     """
@@ -454,14 +468,19 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
     if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
         raise ValueError(f"{fn}: k/v shape mismatch")
     indices, counts = _expand_lists(indices, counts, B, H)
-    kv = _valid_u8(valid, Lk, q.device, fn)
+    if block_mask is not None:
+        block_mask = _check_block_mask(block_mask, Lk, block_n, q.device, fn)
+        kv = None
+    else:
+        kv = _valid_u8(valid, Lk, q.device, fn)
     if out is None:
         out = torch.empty_like(q, memory_format=torch.contiguous_format)
     lse = torch.empty(B, H, Lq, device=q.device, dtype=torch.float32) if return_lse else None
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q.device, fn)
     st = _lib.load().rcsa_sparse_attn_bf16_split(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(kv), scale, _ptr(lse), out.data_ptr(),
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(kv), _ptr(block_mask), scale, _ptr(lse),
+        out.data_ptr(),
         indices.data_ptr(), counts.data_ptr(),
         q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
         v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
@@ -503,11 +522,7 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         raise ValueError(f"{fn}: need {nqb} query and {nkb} key scales per head")
     indices, counts = _expand_lists(indices, counts, B, H)
     if block_mask is not None:
-        if block_mask.dtype != torch.int32 or block_mask.device != q_i8.device \
-                or block_mask.numel() < nkb * (block_n // 32):
-            raise ValueError(f"{fn}: block_mask must be int32 [{nkb}, {block_n // 32}] "
-                             "on the same device")
-        block_mask = block_mask.contiguous()
+        block_mask = _check_block_mask(block_mask, Lk, block_n, q_i8.device, fn)
         kv = None
     else:
         kv = _valid_u8(valid, Lk, q_i8.device, fn)

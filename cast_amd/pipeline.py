@@ -108,10 +108,9 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if int8:  # one launch pools Q (+ int8) and K (+ stats and validity bits)
         qhat, q_i8, q_scale, khat, ksum, kmin, kmax, k_mask = ops.pool_query_key(
             q, q_valid, k, k_valid, bs, q_slot_token=q_slot_token, k_slot_token=k_slot_token)
-    else:
+    else:  # the bf16 attention takes the key validity as bits from the key pooling pass
         qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs)
-        khat, ksum, kmin, kmax = ops.pool_key(k, k_valid, bs)
-        k_mask = None
+        khat, ksum, kmin, kmax, k_mask = ops.pool_key(k, k_valid, bs, block_mask=True)
     # int8 at the layer call's shape: the scores and the top-k run inside the
     # key quantiser's launch (one stream, no cross-stream waits)
     fused = (int8 and fuse_select and order == "index" and k.dtype == torch.bfloat16
@@ -156,8 +155,9 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         qb = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
         kb = k if k.dtype == torch.bfloat16 else k.to(torch.bfloat16)
         vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
-        res = ops.sparse_attn_bf16(qb, kb, vb, idx4, cnt3, k_valid, block_m=bs, block_n=bs,
-                                   sm_scale=scale, return_lse=return_lse, n_split=n_split)
+        res = ops.sparse_attn_bf16(qb, kb, vb, idx4, cnt3, None, block_m=bs, block_n=bs,
+                                   sm_scale=scale, return_lse=return_lse, n_split=n_split,
+                                   block_mask=k_mask)
     out, lse = res if return_lse else (res, None)
     return RCSAResult(out, idx4, cnt3, score, qhat, khat, lse, q_i8, q_scale, k_i8, k_scale,
                       kmean, k_mask)

@@ -299,10 +299,14 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
  *   w_s = l_s 2^(m_s - M),  out = sum_s w_s O_s / sum_s w_s.
  * n_split == 1 is the plain entry point (workspace may be NULL); so is any
  * n_split when every XCD's query blocks fill whole rounds.
+ * The bf16 variant also takes K_block_mask (uint32 [NKB, BLOCK_N / 32], bit i of
+ * word w of block n = validity of key n * BLOCK_N + 32 w + i, 4-byte aligned,
+ * as rcsa_pool_key writes it); when it is not NULL the bits replace K_valid.
  * workspace: 16-byte aligned, at least rcsa_attn_workspace_bytes(...) bytes.
  */
 int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
-                                const uint8_t* K_valid, float sm_scale, float* M,
+                                const uint8_t* K_valid, const uint32_t* K_block_mask,
+                                float sm_scale, float* M,
                                 void* Out, const int32_t* block_indices,
                                 const int32_t* block_indices_lens,
                                 int64_t stride_qz, int64_t stride_qh, int64_t stride_qm,

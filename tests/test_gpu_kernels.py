@@ -272,6 +272,42 @@ def test_sparse_attn_int8_block_mask(dev, D, bs, lk):
     assert torch.equal(lse_b.cpu(), lse_m.cpu())
 
 
+@pytest.mark.parametrize("D,bs,lk,n_split", [(128, 128, 1280, 1), (128, 128, 1189, 1),
+                                              (128, 128, 1189, 3), (64, 64, 640, 1)])
+def test_sparse_attn_bf16_block_mask(dev, D, bs, lk, n_split):
+    """bf16: key validity as bits gives exactly the output of the validity
+    bytes (the 3-slot 64-key-step ring at D 128 and a generic shape), and both
+    agree with the fp32 oracle."""
+    from cast_amd import ops
+    g = torch.Generator().manual_seed(lk + D + n_split)
+    B, H, lq = 1, 3, 3 * bs
+    nkb = -(-lk // bs)
+    k = torch.randn(B, H, nkb * bs, D, generator=g).to(torch.bfloat16)
+    kv = torch.rand(nkb * bs, generator=g) < 0.8
+    kv[lk:] = False
+    kv[2 * bs: 3 * bs] = True
+    kv[3 * bs: 4 * bs] = False
+    kd, kvd = k.to(dev), kv.to(dev)
+    _, _, _, _, mask = ops.pool_key(kd, kvd, bs, block_mask=True)
+    q = torch.randn(B, H, lq, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, H, lk, D, generator=g).to(torch.bfloat16)
+    kk = k[:, :, :lk].contiguous()
+    idx, cnt = _lists((B, H), lq // bs, nkb, nkb, 19)
+    idx[..., 0] = nkb - 1
+    cnt.clamp_(min=1)
+    idx_d, cnt_d = idx.to(dev), cnt.to(dev)
+    args = (q.to(dev), kk.to(dev), v.to(dev), idx_d, cnt_d)
+    by_bytes, lse_b = ops.sparse_attn_bf16(*args, kvd[:lk], block_m=bs, block_n=bs,
+                                           return_lse=True, n_split=n_split)
+    by_bits, lse_m = ops.sparse_attn_bf16(*args, None, block_m=bs, block_n=bs,
+                                          return_lse=True, n_split=n_split, block_mask=mask)
+    assert torch.equal(by_bytes.cpu(), by_bits.cpu())
+    assert torch.equal(lse_b.cpu(), lse_m.cpu())
+    ref, _ = orc.sparse_attention(q.float(), kk.float(), v.float(), idx, cnt, kv[:lk],
+                                  block_m=bs, block_n=bs)
+    _check_out(by_bits, ref, torch.ones(lq, dtype=torch.bool), "bf16 bits vs oracle")
+
+
 def test_pack_unpack_roundtrip(dev):
     from cast_amd import ops
     g = torch.Generator().manual_seed(7)
@@ -343,8 +379,10 @@ def test_sparse_attn_split_lists(dev, int8):
             *kd.stride()[:3], *vd.stride()[:3], *out.stride()[:3], *idx_d.stride()[:3],
             *cnt_d.stride(), B, H, q.shape[2], k.shape[2], D, bs, bs, idx.shape[3]]
     stream = torch.cuda.current_stream().cuda_stream
-    assert lib.rcsa_sparse_attn_bf16_split(*args, 3, small.data_ptr(), need - 256, stream) == 2
-    assert lib.rcsa_sparse_attn_bf16_split(*args, 3, None, need, stream) == 1
+    split_args = args[:4] + [None] + args[4:]  # K_block_mask after K_valid
+    assert lib.rcsa_sparse_attn_bf16_split(*split_args, 3, small.data_ptr(), need - 256,
+                                           stream) == 2
+    assert lib.rcsa_sparse_attn_bf16_split(*split_args, 3, None, need, stream) == 1
     # a K row spanning 16 MiB or more is refused before any launch (the copy
     # addressing multiplies row numbers by the row stride in 24 bits)
     big = list(args)
