@@ -116,9 +116,11 @@ def cpu_baseline(seed: int, heads: int) -> dict:
                           res["counts"].reshape(1, heads, w.n_qblocks)) * w.q.shape[1] / heads
     return {"value": ops / full_s / 1e12, "unit": "TOPS", "cores": torch.get_num_threads(),
             "kind": "port", "ms_per_layer_call": full_s * 1e3,
-            "sample": f"{heads} of 24 heads of the same layer call (fp32 eager: pool, score, "
-                      f"top-k, masked softmax attention), median of 3 after 1 warmup, "
-                      f"scaled x{w.q.shape[1] / heads:g}"}
+            "sample": (f"the whole layer call, all {heads} heads" if heads == w.q.shape[1] else
+                       f"{heads} of {w.q.shape[1]} heads of the layer call, scaled "
+                       f"x{w.q.shape[1] / heads:g}") +
+                      " (fp32 eager: pool, score, top-k, masked softmax attention), "
+                      "median of 3 after 1 warmup"}
 
 
 def compact_layout_call(seed: int, iters: int) -> dict:
@@ -171,10 +173,10 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=8)
-    ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy"], default=None,
-                    help="profiling mode: run only this kernel (--steps launches after "
-                         "--warmup) plus nothing else, and print its average time")
+    ap.add_argument("--cpu-heads", type=int, default=24)
+    ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer"], default=None,
+                    help="profiling mode: run only this kernel (or the whole int8 layer "
+                         "call) --steps times after --warmup, and print its average time")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (the RCSA path needs no collective; "
@@ -200,6 +202,14 @@ def main() -> int:
     w = workloads.matrix_dit(args.seed, int8=args.only != "attn_bf16").to(dev)
     bs = w.block_size
     max_k = w.k_total
+
+    if args.only == "layer":
+        def layer():
+            return rcsa_attention(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=bs,
+                                  k_select=w.k_total, forced=w.forced, int8=True, max_k=max_k)
+        ms = _events_time(layer, args.steps, args.warmup)
+        print(json.dumps({"only": "layer", "avg_ms": ms}))
+        return 0
 
     if args.only is not None:
         r = rcsa_attention(w.q, w.k, w.v, w.q_valid, w.k_valid, block_size=bs,
@@ -229,22 +239,30 @@ def main() -> int:
     first_timed = _prewarm(step, 60.0) + args.warmup
     for _ in range(args.warmup):
         res = step()
-    # HIP events around the attention entry point of every timed step, on the
-    # stream it launches on (torch's current stream): the roofline's launch time
-    attn_events = []
-    entry = ops.sparse_attn_int8
+    # HIP events around the entry points of every timed step, on the stream
+    # they launch on (torch's current stream): the attention's launch time for
+    # the roofline, and the fused pooling and quantiser/selection launches as
+    # they run inside the layer call (K no longer in the MALL from the step before)
+    names = ("sparse_attn_int8", "pool_query_key", "quantize_key_select")
+    events = {n: [] for n in names}
+    entries = {n: getattr(ops, n) for n in names}
 
-    def timed_entry(*a, **kw):
-        ev0 = torch.cuda.Event(enable_timing=True)
-        ev1 = torch.cuda.Event(enable_timing=True)
-        ev0.record()
-        r_ = entry(*a, **kw)
-        ev1.record()
-        attn_events.append((ev0, ev1))
-        return r_
+    def timed(name):
+        entry_ = entries[name]
+
+        def wrapper(*a, **kw):
+            ev0 = torch.cuda.Event(enable_timing=True)
+            ev1 = torch.cuda.Event(enable_timing=True)
+            ev0.record()
+            r_ = entry_(*a, **kw)
+            ev1.record()
+            events[name].append((ev0, ev1))
+            return r_
+        return wrapper
 
     torch.cuda.synchronize()
-    ops.sparse_attn_int8 = timed_entry
+    for n in names:
+        setattr(ops, n, timed(n))
     try:
         t0 = time.perf_counter()
         for _ in range(args.steps):
@@ -252,8 +270,10 @@ def main() -> int:
         torch.cuda.synchronize()
         ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
     finally:
-        ops.sparse_attn_int8 = entry
-    attn_ms = statistics.fmean(a.elapsed_time(b) for a, b in attn_events)
+        for n in names:
+            setattr(ops, n, entries[n])
+    call_ms = {n: statistics.fmean(a.elapsed_time(b) for a, b in ev) for n, ev in events.items()}
+    attn_ms = call_ms["sparse_attn_int8"]
     ops_attn = w.attention_ops(res.indices, res.counts)
     value = ops_attn / (ms_per_step * 1e-3) / 1e12
 
@@ -287,14 +307,17 @@ def main() -> int:
     el = w.q.element_size()
     nbh = B * H
     lk = w.k.shape[2]
-    hbm = {
-        "pool_query_quant": nbh * Lq * D * (el + 1),
-        "pool_key_stats": nbh * lk * D * el + 4 * nbh * w.n_kblocks * D * 4,
-        "quantize_key": nbh * lk * D * (el + 1) + 2 * nbh * w.n_kblocks * D * 4,
-    }
-    hbm_frac = {k_: {"GB/s": b / (stage_ms[k_] * 1e-3) / 1e9,
-                     "frac": b / (stage_ms[k_] * 1e-3) / 1e9 / HBM_PEAK_GBS}
-                for k_, b in hbm.items()}
+    nqb, nkb = w.n_qblocks, w.n_kblocks
+    # algorithmic bytes: every input read once, every output written once
+    pool_q = nbh * Lq * D * (el + 1) + nbh * nqb * (D + 1) * 4
+    pool_k = nbh * lk * D * el + 4 * nbh * nkb * D * 4 + nkb * bs // 8
+    quant_k = nbh * lk * D * (el + 1) + 3 * nbh * nkb * D * 4 + nbh * (nkb + D) * 4
+    select = nbh * (nqb + nkb) * D * 4 + nbh * nqb * (nkb + max_k + 1) * 4
+    hbm_bytes = {"pool_query_key": (pool_q + pool_k, call_ms["pool_query_key"]),
+                 "quantize_key_select": (quant_k + select, call_ms["quantize_key_select"])}
+    hbm_frac = {k_: {"bytes": b, "ms": ms_, "GB/s": b / (ms_ * 1e-3) / 1e9,
+                     "frac": b / (ms_ * 1e-3) / 1e9 / HBM_PEAK_GBS}
+                for k_, (b, ms_) in hbm_bytes.items()}
 
     line = {
         "metric": "block-sparse attn ms/layer-call + effective TOPS, int8-QK, 3.5k q x 35k KV",
@@ -323,7 +346,8 @@ def main() -> int:
     }
     ns_plan = ctypes.c_int64(0)
     _lib.load().rcsa_attn_split_plan(B, H, Lq, bs, max_k, ctypes.byref(ns_plan))
-    extras = {"stage_ms": stage_ms, "hbm": hbm_frac, "ms_per_layer_call": ms_per_step,
+    extras = {"stage_ms": stage_ms, "layer_call_ms": call_ms, "hbm": hbm_frac,
+              "ms_per_layer_call": ms_per_step,
               "attn_split_plan": ns_plan.value,
               "attn_timed_dispatches": [first_timed, args.steps]}
 
