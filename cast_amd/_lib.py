@@ -31,6 +31,8 @@ SIGNATURES: dict[str, list] = {
                                  _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P,
                                  _I, _P, _I, _P, _P],
     "rcsa_row_budgets": [_P, _I, _I, _I, _I, _I, _I, _P, _I, _P],
+    "rcsa_closed_loop_degrees": [_P, _P, _I, _I, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                                 c_float, c_int, c_int, _P, _P, _P],
     "rcsa_select_topk": [_P, _I, _I, _I, _P, _I, _I, _P, _P, _I, _P, _I, _P, c_int, _P],
     "rcsa_quantize_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I, _P, _P, _P,
                           _P, _P, _P, _P],

@@ -221,6 +221,58 @@ def row_budgets(weights: torch.Tensor, total_per_section: int, *, cap: int = 0,
     return out
 
 
+_CL_FEEDBACK = {"additive": 0, "centered_multiplicative": 1, "centered_inverse": 2}
+_CL_ERRORS = ((1, "compact Current frame lies outside CWCA frame capacity"),
+              (4, "compact Closed-Loop Current set contains Memory frames"),
+              (2, "compact Closed-Loop CWCA exhausted key capacity"))
+
+
+def closed_loop_degrees(curvature: torch.Tensor, frames, *, current_temporal_offset: int,
+                        source_group: int, compact_group: int, mean_degree: int,
+                        base_degree: int, total_blocks: int, memory_blocks: int,
+                        response: Optional[torch.Tensor] = None, response_weight: float = 0.0,
+                        feedback_form: str = "additive", fixed_query_budget: bool = False,
+                        check_status: bool = True):
+    """Row degrees of a compact woven layer under the closed-loop allocator
+    (``rcsa_closed_loop_degrees``): int32 ``[total_blocks]`` on the device.
+
+    ``curvature`` / ``response``: float32 ``[T_src, S]``; ``frames``: the active
+    current-local frames (int sequence or tensor).  With ``check_status`` the
+    device status word is read back once and a breach raises ``RuntimeError``
+    with the reference's message; otherwise ``(degrees, status)`` is returned
+    and nothing is read back."""
+    fn = "closed_loop_degrees"
+    _require_cuda(fn, curvature)
+    dev = curvature.device
+    if curvature.dtype != torch.float32 or curvature.ndim != 2:
+        raise TypeError(f"{fn}: curvature must be float32 [T_src, S]")
+    curvature = curvature.contiguous()
+    if response is not None:
+        if response.shape != curvature.shape or response.dtype != torch.float32:
+            raise ValueError(f"{fn}: response must be float32 {tuple(curvature.shape)}")
+        response = response.to(dev).contiguous()
+    if feedback_form not in _CL_FEEDBACK:
+        raise ValueError(f"unknown control-response feedback {feedback_form!r}")
+    fr = torch.as_tensor(frames).to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    degrees = torch.empty(int(total_blocks), device=dev, dtype=torch.int32)
+    status = torch.empty(1, device=dev, dtype=torch.int32)
+    t_src, spatial = curvature.shape
+    st = _lib.load().rcsa_closed_loop_degrees(
+        curvature.data_ptr(), _ptr(response), t_src, spatial, fr.data_ptr(), fr.numel(),
+        int(current_temporal_offset), int(source_group), int(compact_group), int(mean_degree),
+        int(base_degree), int(total_blocks), int(memory_blocks), float(response_weight),
+        _CL_FEEDBACK[feedback_form], int(bool(fixed_query_budget)), degrees.data_ptr(),
+        status.data_ptr(), _stream())
+    check(st, fn)
+    if not check_status:
+        return degrees, status
+    code = int(status.item())
+    for bit, msg in _CL_ERRORS:
+        if code & bit:
+            raise RuntimeError(msg)
+    return degrees
+
+
 def block_scores(qhat: torch.Tensor, khat: torch.Tensor) -> torch.Tensor:
     """``score[bh] = qhat[bh] @ khat[bh]^T`` (P/matrix_curvature_phase_frame_weave.py:5701)."""
     fn = "block_scores"

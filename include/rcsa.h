@@ -123,6 +123,37 @@ int rcsa_pool_query_key(const void* q, const void* k, int dtype, int64_t batch,
                         uint32_t* block_mask, hipStream_t stream);
 
 /*
+ * Row degrees of a compact woven layer under the closed-loop allocator, on the
+ * device (no .item() syncs).  Replaces compact_closed_loop_degrees
+ * (P/control_response_cwca_attention.py:1188-1363, with _compact_time_cells
+ * :1123-1163 and _redistribute_compact_capacity :1165-1186) and its
+ * composition into the layer's degrees (P/matrix_curvature_phase_frame_weave.py:
+ * 5727-5817):
+ *   curvature [t_src][spatial] fp32 (the compiler's curvature matrix), response
+ *   [t_src][spatial] fp32 or NULL (the previous layer's response; ignored when
+ *   response_weight == 0), frames [n_frames] int32 current-local active frames,
+ *   current_temporal_offset, source_group (the block shape's tt of the CWCA
+ *   tiles), compact_group (the compact tt), feedback_form 0 additive,
+ *   1 centered multiplicative, 2 centered inverse; fixed_query_budget != 0 gives
+ *   every current cell mean_degree.
+ * degrees: int32 [total_blocks]; total_blocks == memory_blocks +
+ * ceil(n_frames / compact_group) * spatial (the packed rows).  status: int32 [1],
+ * written on the device: 0, or the bits RCSA_CL_OUTSIDE_TILES (a profiled frame
+ * lies past the curvature tiles), RCSA_CL_EXHAUSTED (a worldline ran out of key
+ * capacity: the reference raises "exhausted key capacity") and
+ * RCSA_CL_MEMORY_FRAME (a negative, i.e. memory, frame).  spatial <= 1024, at
+ * most 64 cells, total_blocks <= 8192.
+ */
+enum { RCSA_CL_OUTSIDE_TILES = 1, RCSA_CL_EXHAUSTED = 2, RCSA_CL_MEMORY_FRAME = 4 };
+int rcsa_closed_loop_degrees(const float* curvature, const float* response, int64_t t_src,
+                             int64_t spatial, const int32_t* frames, int64_t n_frames,
+                             int64_t current_temporal_offset, int64_t source_group,
+                             int64_t compact_group, int64_t mean_degree, int64_t base_degree,
+                             int64_t total_blocks, int64_t memory_blocks, float response_weight,
+                             int feedback_form, int fixed_query_budget, int32_t* degrees,
+                             int32_t* status, hipStream_t stream);
+
+/*
  * Per-row key-block budgets on the device, so no budget is read back to the
  * host.  For every section row s of weights [n_sections][n] (row stride
  * weights_stride): largest-remainder apportionment of total_per_section edges

@@ -21,6 +21,15 @@ docstring; the pins live in tests/test_oracle_pins.py:
   apportion*          exact rational arithmetic (fractions.Fraction) + conserved sums
   saturate            closed forms: the result sums to min(target, n * cap), never
                       exceeds cap, and only rows below cap before a pass gain
+  compact_time_cells  hand-computed cells (profiled / unprofiled frames, partial
+                      last cell); out-of-tile frames raise
+  redistribute_compact_capacity
+                      closed forms: worldline sums reach the target, no row
+                      above capacity, raises exactly when capacity runs out
+  closed_loop_degrees conserved edge budgets (every worldline Tc * mean, the
+                      whole layer blocks * mean); uniform curvature gives
+                      uniform degrees; a pure-Python Fraction re-derivation
+                      on small cases
 """
 from __future__ import annotations
 
@@ -35,6 +44,8 @@ __all__ = [
     "quantize_query_blocks", "key_mean", "quantize_key_blocks", "dequantize_blocks",
     "sparse_attention", "sparse_attention_int8", "equivalence_stats", "compact_layout",
     "apportion", "apportion_section_matrix", "saturate", "budget_blocks", "rcsa_layer",
+    "apportion_section_matrix_f32", "compact_time_cells", "redistribute_compact_capacity",
+    "closed_loop_degrees",
 ]
 
 
@@ -405,6 +416,128 @@ def saturate(degrees: Sequence[int], cap: int, target_total: int) -> list[int]:
         if gave == 0:
             break
     return d
+
+
+def apportion_section_matrix_f32(weights: torch.Tensor, total_per_section: int) -> torch.Tensor:
+    """Row-wise largest remainder in fp32 torch arithmetic, as
+    P/qk_uncertainty_tangent_attention.py:1239-1264 computes it (clamp_min(0),
+    a non-positive row weighs every entry 1, raw = total * w / sum, floor, one
+    more edge to the largest fractional parts by a stable descending sort)."""
+    normalized = weights.float().clamp_min(0.0)
+    normalized = torch.where(normalized.sum(dim=-1, keepdim=True) > 0, normalized,
+                             torch.ones_like(normalized))
+    raw = float(total_per_section) * normalized / normalized.sum(dim=-1, keepdim=True)
+    result = torch.floor(raw).to(torch.long)
+    remainder = total_per_section - result.sum(dim=-1)
+    fractions = raw - result
+    order = torch.argsort(fractions, dim=-1, descending=True, stable=True)
+    ranks = torch.empty_like(order)
+    ranks.scatter_(-1, order, torch.arange(weights.shape[-1])[None].expand_as(order))
+    return result + (ranks < remainder[:, None]).to(result.dtype)
+
+
+def compact_time_cells(values: torch.Tensor, active_current_local: Sequence[int],
+                       compact_group: int, source_group: int, offset: int) -> torch.Tensor:
+    """Per-worldline signal of the compact current time cells.
+
+    Restates P/control_response_cwca_attention.py:1123-1163: frame f (current
+    local) reads source tile floor((f - offset) / source_group) of ``values``
+    [T_src, S] when f >= offset, else 0; each run of ``compact_group`` frames
+    is averaged into one cell.  Returns [T_cells, S]."""
+    local = torch.as_tensor(list(active_current_local), dtype=torch.long)
+    profiled = local >= int(offset)
+    cells = torch.div((local - int(offset)).clamp_min(0), int(source_group),
+                      rounding_mode="floor")
+    if bool(torch.any(profiled & (cells >= int(values.shape[0])))):
+        raise RuntimeError("compact Current frame lies outside CWCA tiles")
+    selected = torch.zeros(int(local.numel()), int(values.shape[1]), dtype=values.dtype)
+    if bool(profiled.any()):
+        selected[profiled] = values.index_select(0, cells[profiled])
+    rows = [selected[lo:lo + int(compact_group)].mean(dim=0)
+            for lo in range(0, int(selected.shape[0]), int(compact_group))]
+    if not rows:
+        raise RuntimeError("compact Closed-Loop CWCA has no Current cells")
+    return torch.stack(rows)
+
+
+def redistribute_compact_capacity(degrees: torch.Tensor, *, capacity: int,
+                                  target_per_worldline: int) -> torch.Tensor:
+    """Clamp every cell to ``capacity``, then per worldline (column) give the
+    lost edges one each to the lowest cells below capacity, pass after pass;
+    raise when a worldline has no room left
+    (P/control_response_cwca_attention.py:1165-1186)."""
+    degrees = degrees.clamp(max=capacity)
+    for s in range(int(degrees.shape[1])):
+        missing = target_per_worldline - int(degrees[:, s].sum())
+        while missing > 0:
+            cand = torch.nonzero(degrees[:, s] < capacity).flatten()
+            if not int(cand.numel()):
+                raise RuntimeError("compact Closed-Loop CWCA exhausted key capacity")
+            take = min(missing, int(cand.numel()))
+            degrees[cand[:take], s] += 1
+            missing -= take
+    return degrees
+
+
+def closed_loop_degrees(curvature: torch.Tensor, active_current_local: Sequence[int], *,
+                        current_temporal_offset: int, source_group: int, compact_group: int,
+                        mean_degree: int, base_degree: int, total_blocks: int,
+                        memory_blocks: int, response: Optional[torch.Tensor] = None,
+                        response_weight: float = 0.0, feedback_form: str = "additive",
+                        fixed_query_budget: bool = False, layer_index: int = 1) -> torch.Tensor:
+    """Row degrees of a compact woven layer under the closed-loop allocator.
+
+    Restates compact_closed_loop_degrees (P/control_response_cwca_attention.py:
+    1188-1363) and how the frame weave composes it
+    (P/matrix_curvature_phase_frame_weave.py:5727-5817): memory rows keep
+    ``mean_degree``; the current cells get base + the largest-remainder split of
+    Tc * (mean - base) edges per spatial worldline by 1 + log1p(signal), where
+    the signal is the column-normalised curvature of the compact cells (plus the
+    previous layer's response with the closed-loop feedback form); each
+    worldline is saturated at ``total_blocks`` and redistributed; then the whole
+    layer is clamped and saturated to ``total_blocks * mean_degree``.
+    ``curvature`` / ``response``: [T_src, S] fp32.  Returns int64 [total_blocks].
+    """
+    cur = curvature.float()
+    spatial = int(cur.shape[1])
+    eps = torch.finfo(cur.dtype).eps
+    current_capacity = int(current_temporal_offset) + int(cur.shape[0]) * int(source_group)
+    local = [int(f) for f in active_current_local]
+    if not local:
+        raise RuntimeError("compact Closed-Loop has no active Current frames")
+    if any(f < 0 for f in local):
+        raise RuntimeError("compact Closed-Loop Current set contains Memory frames")
+    if any(f >= current_capacity for f in local):
+        raise RuntimeError("compact Current frame lies outside CWCA frame capacity")
+    normalized = cur / cur.mean(dim=0, keepdim=True).clamp_min(eps)
+    compact = compact_time_cells(normalized, local, compact_group, source_group,
+                                 current_temporal_offset)
+    cells = int(compact.shape[0])
+    if fixed_query_budget:
+        current = torch.full((cells, spatial), int(mean_degree), dtype=torch.long)
+    else:
+        if layer_index == 0 or response_weight == 0.0 or response is None:
+            signal = compact
+        else:
+            resp = compact_time_cells(response.float(), local, compact_group, source_group,
+                                      current_temporal_offset)
+            if feedback_form == "additive":
+                signal = compact + response_weight * resp
+            else:
+                sign = -1.0 if feedback_form == "centered_inverse" else 1.0
+                signal = compact * torch.exp(sign * response_weight * (resp - 1.0))
+        weights = 1.0 + torch.log1p(signal)
+        residual = cells * (int(mean_degree) - int(base_degree))
+        bonus = apportion_section_matrix_f32(weights.transpose(0, 1), residual).transpose(0, 1)
+        current = redistribute_compact_capacity(bonus + int(base_degree),
+                                                capacity=int(total_blocks),
+                                                target_per_worldline=cells * int(mean_degree))
+    if int(current.numel()) != int(total_blocks) - int(memory_blocks):
+        raise RuntimeError("compact Closed-Loop degree layout differs from packed rows")
+    degrees = torch.full((int(total_blocks),), int(mean_degree), dtype=torch.long)
+    degrees[int(memory_blocks):] = current.reshape(-1)
+    return torch.tensor(saturate(degrees.tolist(), int(total_blocks),
+                                 int(total_blocks) * int(mean_degree)), dtype=torch.long)
 
 
 def budget_blocks(fraction: float, n_history_blocks: int) -> int:

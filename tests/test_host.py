@@ -41,7 +41,7 @@ def test_library_exports_every_declared_symbol(lib):
 def test_status_strings_and_version(lib):
     # host-only entry points: no device work
     assert lib.rcsa_abi_version() >> 16 >= 1
-    for code in range(7):
+    for code in range(8):
         assert lib.rcsa_status_string(code)
     assert b"unknown" in lib.rcsa_status_string(99).lower()
     with pytest.raises(RuntimeError, match=r"rcsa_demo: .*\(status 2\)"):

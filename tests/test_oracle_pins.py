@@ -529,3 +529,106 @@ def test_saturate_pins():
                     assert gain[j] >= gain[i]
     # a hand case: 2 edges lost to the cap go to rows 1 and 2
     assert orc.saturate([12, 1, 1], 10, 14) == [10, 2, 2]
+
+
+# --------------------------------------------------------------------------
+# closed-loop allocator (P/control_response_cwca_attention.py:1123-1363 and
+# P/matrix_curvature_phase_frame_weave.py:5727-5817)
+
+def test_compact_time_cells_hand_example():
+    vals = torch.tensor([[1.0, 10.0], [2.0, 20.0], [3.0, 30.0]])
+    # offset 3, source tiles of 4 frames: frames 0-2 are unprofiled (0), 3-6
+    # read tile 0, 7-10 tile 1, 11-14 tile 2; cells of 2 frames
+    got = orc.compact_time_cells(vals, [1, 3, 7, 8, 14], 2, 4, 3)
+    want = torch.tensor([[(0 + 1) / 2, (0 + 10) / 2], [(2 + 2) / 2, (20 + 20) / 2], [3.0, 30.0]])
+    assert torch.allclose(got, want)
+    with pytest.raises(RuntimeError, match="outside CWCA tiles"):
+        orc.compact_time_cells(vals, [15], 2, 4, 3)
+
+
+def test_redistribute_closed_forms():
+    g = torch.Generator().manual_seed(4)
+    for _ in range(50):
+        cells, S, cap = 4, 6, int(torch.randint(5, 12, (1,), generator=g))
+        d = torch.randint(0, 20, (cells, S), generator=g)
+        target = int(torch.randint(0, cells * cap + 1, (1,), generator=g))
+        out = orc.redistribute_compact_capacity(d.clone(), capacity=cap,
+                                                target_per_worldline=target)
+        assert int(out.max()) <= cap
+        for s in range(S):
+            col0 = d[:, s].clamp(max=cap)
+            want = max(target, int(col0.sum()))  # edges are only added, never removed
+            assert int(out[:, s].sum()) == want
+            assert torch.all(out[:, s] >= col0)
+    with pytest.raises(RuntimeError, match="exhausted key capacity"):
+        orc.redistribute_compact_capacity(torch.zeros(2, 1, dtype=torch.long), capacity=3,
+                                          target_per_worldline=7)
+
+
+def _fraction_closed_loop(curv, frames, offset, src, grp, mean, base, blocks, mem):
+    """The allocation re-derived with exact rationals on the oracle's fp32 weights."""
+    from fractions import Fraction
+    cur = curv.float()
+    norm = cur / cur.mean(dim=0, keepdim=True).clamp_min(torch.finfo(torch.float32).eps)
+    cells = orc.compact_time_cells(norm, frames, grp, src, offset)
+    w = (1.0 + torch.log1p(cells)).tolist()
+    tc, S = len(w), len(w[0])
+    deg = [[0] * S for _ in range(tc)]
+    for s in range(S):
+        col = [max(Fraction(w[c][s]), Fraction(0)) for c in range(tc)]
+        share = orc.apportion([float(x) for x in col], tc * (mean - base))
+        for c in range(tc):
+            deg[c][s] = share[c] + base
+    full = [mean] * mem + [deg[c][s] for c in range(tc) for s in range(S)]
+    assert len(full) == blocks
+    return full
+
+
+def test_closed_loop_conservation_and_rationals():
+    g = torch.Generator().manual_seed(9)
+    for trial in range(20):
+        S, tsrc = 6, 3
+        curv = torch.rand(tsrc, S, generator=g) * 2 + 0.05
+        frames = sorted(torch.randperm(14, generator=g)[:8].tolist())
+        cells = -(-len(frames) // 4)
+        mem, mean, base = 2 * S, 7, 5
+        blocks = mem + cells * S
+        d = orc.closed_loop_degrees(curv, frames, current_temporal_offset=2, source_group=4,
+                                    compact_group=4, mean_degree=mean, base_degree=base,
+                                    total_blocks=blocks, memory_blocks=mem)
+        assert int(d.sum()) == blocks * mean
+        assert torch.all(d[:mem] == mean)
+        cur = d[mem:].reshape(cells, S)
+        assert torch.all(cur.sum(0) == cells * mean) and torch.all(cur >= base)
+        exact = _fraction_closed_loop(curv, frames, 2, 4, 4, mean, base, blocks, mem)
+        assert d.tolist() == exact, trial
+
+
+def test_closed_loop_uniform_and_slips():
+    # uniform curvature: every cell of a worldline gets the same bonus when it divides
+    curv = torch.full((2, 5), 0.7)
+    d = orc.closed_loop_degrees(curv, [0, 1, 2, 3, 4, 5, 6, 7], current_temporal_offset=0,
+                                source_group=4, compact_group=4, mean_degree=9, base_degree=7,
+                                total_blocks=10 + 10, memory_blocks=10)
+    assert torch.all(d == 9)
+    # a planted slip -- no per-worldline column normalisation -- changes the split
+    g = torch.Generator().manual_seed(2)
+    curv = torch.rand(3, 6, generator=g) * torch.tensor([1.0, 3.0, 9.0, 0.2, 5.0, 1.0])
+    kw = dict(current_temporal_offset=0, source_group=4, compact_group=4, mean_degree=30,
+              base_degree=24, total_blocks=18 + 18, memory_blocks=18)
+    frames = list(range(12))
+    good = orc.closed_loop_degrees(curv, frames, **kw)
+    slip = orc.closed_loop_degrees(curv / curv.mean(dim=0, keepdim=True), frames, **kw)
+    assert torch.equal(good, slip)  # the normalisation is idempotent ...
+    raw_w = 1.0 + torch.log1p(orc.compact_time_cells(curv, frames, 4, 4, 0))
+    raw = orc.apportion_section_matrix_f32(raw_w.transpose(0, 1), 3 * 6).transpose(0, 1) + 24
+    assert not torch.equal(good[18:].reshape(3, 6), raw)  # ... and dropping it is caught
+    # the fixed query budget ignores the curvature
+    fixed = orc.closed_loop_degrees(curv, frames, fixed_query_budget=True, **kw)
+    assert torch.all(fixed == 30)
+    # response feedback moves edges towards responsive cells (additive form)
+    resp = torch.zeros(3, 6)
+    resp[1] = 5.0
+    fb = orc.closed_loop_degrees(curv, frames, response=resp, response_weight=1.0, **kw)
+    cur, base_cur = fb[18:].reshape(3, 6), good[18:].reshape(3, 6)
+    assert torch.all(cur[1] >= base_cur[1]) and int(cur[1].sum()) > int(base_cur[1].sum())
