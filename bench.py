@@ -123,12 +123,12 @@ def cpu_baseline(seed: int, heads: int) -> dict:
                       "median of 3 after 1 warmup"}
 
 
-def compact_layout_call(seed: int, iters: int) -> dict:
-    """The int8 layer call on token-major Q/K/V of the Matrix latent grid (22 x 40
+def _compact_calls(seed: int, int8: bool = True):
+    """The layer call (int8, or bf16) on token-major Q/K/V of the Matrix latent grid (22 x 40
     tokens per frame, (4, 4, 8) tiles with 64-token bottom tiles; 4 query frames,
     40 memory + 4 current key frames; 24 heads, D 128; history budget 25% + the
-    current blocks): packing fused into the kernels (slot maps) against
-    pack_tokens -> packed layer call -> unpack_tokens."""
+    current blocks): (packing fused into the kernels through slot maps,
+    pack_tokens -> packed layer call -> unpack_tokens, sizes)."""
     import torch
     from cast_amd import layout, ops
     from cast_amd.pipeline import rcsa_attention
@@ -141,28 +141,40 @@ def compact_layout_call(seed: int, iters: int) -> dict:
     q, k, v = (torch.randn(1, n, H, D, device=dev, generator=g).div_(D ** 0.5)
                .to(torch.bfloat16) for n in (lq, lk, lk))
     nq, nk = lay_q.n_blocks, lay_k.n_blocks
-    forced = torch.zeros(nq, nk, dtype=torch.bool)
+    forced = torch.zeros(nq, nk, dtype=torch.bool, device=dev)
     forced[:, nk - 30:] = True
     k_sel = round(0.25 * (nk - 30)) + 30
 
     def fused():
         return rcsa_attention(q, k, v, None, None, block_size=128, k_select=k_sel,
-                              forced=forced, int8=True, max_k=k_sel,
-                              q_slot_token=lay_q.slot_token, k_slot_token=lay_k.slot_token).out
+                              forced=forced, int8=int8, max_k=k_sel,
+                              q_slot_token=lay_q.slot_token32,
+                              k_slot_token=lay_k.slot_token32).out
 
     def unfused():
         r = rcsa_attention(ops.pack_tokens(q, lay_q.slot_token), ops.pack_tokens(k, lay_k.slot_token),
                            ops.pack_tokens(v, lay_k.slot_token), lay_q.slot_valid,
                            lay_k.slot_valid, block_size=128, k_select=k_sel, forced=forced,
-                           int8=True, max_k=k_sel)
+                           int8=int8, max_k=k_sel)
         return ops.unpack_tokens(r.out, lay_q.token_to_packed)
 
-    same = bool(torch.equal(fused(), unfused()))
-    _prewarm(fused, 40.0)
-    f_ms = _events_time(fused, iters)
-    u_ms = _events_time(unfused, iters)
-    return {"fused_ms": f_ms, "pack_unpack_ms": u_ms, "outputs_equal": same,
-            "q_blocks": nq, "k_blocks": nk, "k_select": k_sel}
+    return fused, unfused, {"q_blocks": nq, "k_blocks": nk, "k_select": k_sel}
+
+
+def compact_layout_call(seed: int, iters: int) -> dict:
+    """The gathered layer call against pack -> packed call -> unpack (int8,
+    then the bf16 drop-in)."""
+    import torch
+    res = {}
+    for int8 in (True, False):
+        fused, unfused, sizes = _compact_calls(seed, int8)
+        same = bool(torch.equal(fused(), unfused()))
+        _prewarm(fused, 40.0)
+        f_ms = _events_time(fused, iters)
+        u_ms = _events_time(unfused, iters)
+        res["int8" if int8 else "bf16"] = {"fused_ms": f_ms, "pack_unpack_ms": u_ms,
+                                           "outputs_equal": same}
+    return {**res, **sizes}
 
 
 def main() -> int:
@@ -174,9 +186,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=24)
-    ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer"], default=None,
+    ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer", "compact",
+                                       "compact_bf16"],
+                    default=None,
                     help="profiling mode: run only this kernel (or the whole int8 layer "
-                         "call) --steps times after --warmup, and print its average time")
+                         "call, or the gathered call on the Matrix latent grid) --steps "
+                         "times after --warmup, and print its average time")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (the RCSA path needs no collective; "
@@ -197,6 +212,12 @@ def main() -> int:
         ms = _events_time(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"only": "copy", "bytes_read": src.numel() * 4,
                           "bytes_written": dst.numel() * 4, "avg_ms": ms}))
+        return 0
+
+    if args.only in ("compact", "compact_bf16"):
+        fused, _, sizes = _compact_calls(args.seed, args.only == "compact")
+        ms = _events_time(fused, args.steps, args.warmup)
+        print(json.dumps({"only": args.only, "avg_ms": ms, **sizes}))
         return 0
 
     w = workloads.matrix_dit(args.seed, int8=args.only != "attn_bf16").to(dev)
@@ -407,6 +428,17 @@ def main() -> int:
             "30x28": 1e3 * _events_time(lambda: ops.row_budgets(w30, 28 * 69, cap=303), iters),
             "1x853": 1e3 * _events_time(lambda: ops.row_budgets(w853, 853 * 64, cap=853),
                                         iters)}
+        # closed-loop degrees of a compact woven layer: 30 worldlines (6 x 5
+        # spatial tiles), 16 current frames in 4 cells after 183 memory rows,
+        # with the previous layer's response fed back; status left on the device
+        curv = torch.rand(4, 30, device=dev, generator=gb) + 0.05
+        resp = torch.rand(4, 30, device=dev, generator=gb) * 2
+        cl_kw = dict(current_temporal_offset=3, source_group=4, compact_group=4,
+                     mean_degree=61, base_degree=49, total_blocks=303, memory_blocks=183,
+                     response=resp, response_weight=0.5, check_status=False)
+        frames_d = torch.arange(3, 19, device=dev, dtype=torch.int32)
+        extras["row_budgets_us"]["closed_loop_303"] = 1e3 * _events_time(
+            lambda: ops.closed_loop_degrees(curv, frames_d, **cl_kw), iters)
 
     line["extras"] = extras
     if not args.no_cpu_baseline:

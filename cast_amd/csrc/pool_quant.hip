@@ -270,11 +270,12 @@ pool_kernel(PoolArgs a) {
 // statistics) in one launch: the first q_tiles workgroups take query tiles,
 // the rest key tiles.  The short, latency-bound query pass then runs inside
 // the HBM-bound key pass instead of before it.
-template <typename T, int D, int BS, bool MAP>
+// (QS false: the bf16 path's pooling, no query quantiser and no key statistics)
+template <typename T, int D, int BS, bool MAP, bool QS = true>
 __global__ void __launch_bounds__(kPoolThreads)
 pool_qk_kernel(PoolArgs q, PoolArgs k, int64_t q_tiles) {
-  if (blockIdx.x < q_tiles) pool_tile<T, D, BS, true, false, MAP>(q, blockIdx.x);
-  else pool_tile<T, D, BS, false, true, MAP>(k, blockIdx.x - q_tiles);
+  if (blockIdx.x < q_tiles) pool_tile<T, D, BS, QS, false, MAP>(q, blockIdx.x);
+  else pool_tile<T, D, BS, false, QS, MAP>(k, blockIdx.x - q_tiles);
 }
 
 // Cosine scores: one workgroup per (bh, 16 query blocks, 64 key blocks).
@@ -375,7 +376,35 @@ kmean_kernel(const float* ksum, const uint8_t* valid, const int32_t* slot_tok,
   part[bl][c] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
   int cnt = 0;
   if (slot_tok != nullptr) {  // gathered keys: a slot counts when it holds a token
-    for (int64_t i = t; i < n_tokens; i += 256) {
+    // four slots per 16-byte load (and their four validity bytes per word),
+    // eight loads in flight per thread
+    const uint32_t src = static_cast<uint32_t>(src_len);
+    const bool vec = (reinterpret_cast<uintptr_t>(slot_tok) & 15u) == 0 &&
+                     (valid == nullptr || (reinterpret_cast<uintptr_t>(valid) & 3u) == 0);
+    const int64_t n4 = vec ? n_tokens / 4 : 0;
+    const int4* s4 = reinterpret_cast<const int4*>(slot_tok);
+    const uint32_t* v4 = reinterpret_cast<const uint32_t*>(valid);
+    auto count4 = [&](int4 w, uint32_t vb) {
+      return static_cast<int>(static_cast<uint32_t>(w.x) < src && (vb & 0xffu)) +
+             static_cast<int>(static_cast<uint32_t>(w.y) < src && (vb & 0xff00u)) +
+             static_cast<int>(static_cast<uint32_t>(w.z) < src && (vb & 0xff0000u)) +
+             static_cast<int>(static_cast<uint32_t>(w.w) < src && (vb & 0xff000000u));
+    };
+    int64_t i0 = t;
+    for (; i0 + 7 * 256 < n4; i0 += 8 * 256) {
+      int4 w[8];
+      uint32_t vb[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        w[k] = s4[i0 + k * 256];
+        vb[k] = valid == nullptr ? 0xffffffffu : v4[i0 + k * 256];
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) cnt += count4(w[k], vb[k]);
+    }
+    for (; i0 < n4; i0 += 256)
+      cnt += count4(s4[i0], valid == nullptr ? 0xffffffffu : v4[i0]);
+    for (int64_t i = n4 * 4 + t; i < n_tokens; i += 256) {
       const int32_t tk = slot_tok[i];
       cnt += tk >= 0 && tk < src_len && (valid == nullptr || valid[i] != 0);
     }
@@ -583,8 +612,10 @@ extern "C" int rcsa_pool_query_key(
     const int32_t* q_slot_token, int64_t q_src_len, const int32_t* k_slot_token,
     int64_t k_src_len, float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum,
     float* kmin, float* kmax, uint32_t* block_mask, hipStream_t stream) {
-  if (!q || !k || !qhat || !q_i8 || !q_scale || !khat || !ksum || !kmin || !kmax)
-    return RCSA_ERR_NULL;
+  if (!q || !k || !qhat || !khat) return RCSA_ERR_NULL;
+  // the quantiser outputs and the key statistics come together or not at all
+  const bool qs = q_i8 || q_scale || ksum || kmin || kmax;
+  if (qs && !(q_i8 && q_scale && ksum && kmin && kmax)) return RCSA_ERR_NULL;
   // both gathered or neither (one kernel instance serves both tile kinds)
   if ((q_slot_token == nullptr) != (k_slot_token == nullptr)) return RCSA_ERR_NULL;
   const bool map = q_slot_token != nullptr;
@@ -609,7 +640,9 @@ extern "C" int rcsa_pool_query_key(
   const int64_t q_tiles = nbh * n_qblocks;
   const dim3 grid(static_cast<unsigned>(q_tiles + nbh * n_kblocks)), block(kPoolThreads);
 #define RCSA_PQK(T_, D_, BS_)                                                     \
-  if (map) pool_qk_kernel<T_, D_, BS_, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles); \
+  if (!qs) { if (map) pool_qk_kernel<T_, D_, BS_, true, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles); \
+             else pool_qk_kernel<T_, D_, BS_, false, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles); } \
+  else if (map) pool_qk_kernel<T_, D_, BS_, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles); \
   else pool_qk_kernel<T_, D_, BS_, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles)
 #define RCSA_PQK_T(T_)                                               \
   if (head_dim == 128 && block_size == 128) { RCSA_PQK(T_, 128, 128); } \

@@ -72,6 +72,12 @@ struct AttnArgs {
   // Out and M (out_len rows per (b, h)); -1 or a row >= out_len is dropped.
   const int32_t* out_tok;
   int64_t out_len;
+  // Gathered sources (GATHER kernels only): packed key slot s reads row
+  // kv_tok[s] of a token-major V (and, bf16, K) with kv_len token rows; -1
+  // or a row >= kv_len is an empty slot (zeros).  bf16 Q rows come through
+  // out_tok (the same query map the output is written through).
+  const int32_t* kv_tok;
+  int64_t kv_len;
 };
 
 // Output row of packed query row r, or -1 when the row is not written.
@@ -221,7 +227,8 @@ constexpr int attn_waves_min() {
 template <bool INT8, int D, int BN, int STAGES, int BNS, int NKH>
 constexpr int attn_waves_max() { return attn_two_wg<INT8, D, BN, STAGES, BNS>() ? 2 * NKH : 8; }
 
-template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH, bool MASK>
+template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH, bool MASK,
+          bool GATHER = false>
 __global__ void __launch_bounds__(BM * 2 * NKH)  // == AttnCfg::NT
 __attribute__((amdgpu_waves_per_eu(attn_waves_min<INT8, D, BN, STAGES, BNS, NKH, BM * 2 * NKH>(),
                                    attn_waves_max<INT8, D, BN, STAGES, BNS, NKH>())))
@@ -235,6 +242,12 @@ sparse_attn_kernel(AttnArgs a) {
   // validity bits (MASK: read with scalar loads instead)
   constexpr bool kValidCopy = kDmaInPv && !MASK;
   constexpr int kOps = C::DMA + (kValidCopy ? 1 : 0);
+  // GATHER: every ring step also reads, one step ahead, the slot-map entries
+  // of the VUPW V rows (bf16: and the same K rows) its lane copies
+  constexpr int kTok = GATHER ? C::VUPW : 0;
+  static_assert(!GATHER || (kDmaInPv && MASK), "gathered sources ride the 3-slot ring with bits");
+  static_assert(!GATHER || INT8 || (C::KUPW == C::VUPW && C::K_RPU == C::V_RPU &&
+                                    C::CPR_K == C::CPR_V), "bf16 K and V rows share tokens");
   typedef typename std::conditional<INT8, v16i, v16f>::type AccT;
   // Ring slots are separate arrays and the loop is unrolled over them, so
   // the compiler can prove that reads of slot j do not alias the copies in
@@ -273,7 +286,13 @@ sparse_attn_kernel(AttnArgs a) {
   const int rg = wave % C::NRG, kh = wave / C::NRG;
   const int hf = lane >> 5, lr = lane & 31;
   const int64_t qrow = qb * BM + rg * 32 + lr;
-  const bool qrow_ok = qrow < a.q_len;
+  bool qrow_ok = qrow < a.q_len;
+  int64_t qsrc = qrow;  // source row of the Q load
+  if constexpr (GATHER && !INT8) {  // bf16 queries are read through the query map
+    const int32_t t = qrow_ok ? a.out_tok[qrow] : -1;
+    qrow_ok = t >= 0 && t < a.out_len;
+    qsrc = t;
+  }
 
   // Workgroup-uniform list length and query-block scale, through the scalar
   // cache, issued ahead of the Q loads so the two latencies overlap.
@@ -285,7 +304,7 @@ sparse_attn_kernel(AttnArgs a) {
   OpT q_op[C::QSTEPS];
   {
     const char* qp = static_cast<const char*>(a.q) +
-                     (b * a.sqz + h * a.sqh + qrow * a.sqm) * C::KB;
+                     (b * a.sqz + h * a.sqh + qsrc * a.sqm) * C::KB;
 #pragma unroll
     for (int st = 0; st < C::QSTEPS; ++st) {
       v4i raw = {0, 0, 0, 0};
@@ -333,13 +352,16 @@ sparse_attn_kernel(AttnArgs a) {
   auto v_row = [&](int i) __attribute__((always_inline)) { return (wave * C::VUPW + i) * C::V_RPU + lane / C::CPR_V; };
   auto k_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_K) ^ (swz_k<C::KROW>(k_row(i)) & (C::CPR_K - 1))) * 16; };
   auto v_col = [&](int i) __attribute__((always_inline)) { return ((lane % C::CPR_V) ^ (swz_v(v_row(i)) & (C::CPR_V - 1))) * 16; };
+  // (gathered rows: the row part comes from the slot map at copy time, so
+  // only the column part is kept)
+  constexpr bool kGatherK = GATHER && !INT8;
   uint32_t k_lo[C::KUPW], v_lo[C::VUPW];
 #pragma unroll
   for (int i = 0; i < C::KUPW; ++i)
-    k_lo[i] = static_cast<uint32_t>(k_row(i) * krow_bytes) + k_col(i);
+    k_lo[i] = (kGatherK ? 0u : static_cast<uint32_t>(k_row(i) * krow_bytes)) + k_col(i);
 #pragma unroll
   for (int i = 0; i < C::VUPW; ++i)
-    v_lo[i] = static_cast<uint32_t>(v_row(i) * vrow_bytes) + v_col(i);
+    v_lo[i] = (GATHER ? 0u : static_cast<uint32_t>(v_row(i) * vrow_bytes)) + v_col(i);
   // Copy step n (BNS keys from key n*BNS; clamped to 0 when invalid) into a
   // slot.  Rows past k_len re-read the last row (those keys are masked).
   // (Named source pointers: an inline pointer expression as this builtin's
@@ -350,7 +372,54 @@ sparse_attn_kernel(AttnArgs a) {
   // keys are masked); the copies then sit in the caller's basic block
   // between its MFMAs.
   const uint32_t krb = static_cast<uint32_t>(krow_bytes), vrb = static_cast<uint32_t>(vrow_bytes);
-  auto stage_flat = [&](int n, char* dst) __attribute__((always_inline)) {
+  // Gathered rows: lane l of copy i moves a chunk of slot v_row(i) =
+  // v_row(0) + i V_RPU of the step, read from the slot map through a buffer
+  // resource (map entries past K_LEN read as 0: none are asked for).  A row
+  // goes through a resource over the whole (b, h) plane of the token-major
+  // source (kv_len rows; the host keeps kv_len x row bytes below 2^31), and an
+  // empty slot gets an offset past its end, so it lands as zeros.
+  constexpr int kTokArr = kTok > 0 ? kTok : 1;
+  const uint32_t kv_rows = static_cast<uint32_t>(a.kv_len);
+  const uint32_t tok_lane = static_cast<uint32_t>(v_row(0)) * 4u;
+  auto load_tokens = [&](int n, uint32_t (&tk)[kTokArr]) __attribute__((always_inline)) {
+    if constexpr (GATHER) {
+      const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<int32_t*>(a.kv_tok), 0, klen * 4, kRsrcWord3);
+      const int key0 = (n < 0 ? 0 : n) * BNS;
+#pragma unroll
+      for (int i = 0; i < kTok; ++i)
+        tk[i] = static_cast<uint32_t>(__builtin_amdgcn_raw_buffer_load_b32(
+            r, static_cast<int>(tok_lane) + i * C::V_RPU * 4, key0 * 4, 0));
+    }
+  };
+  auto row_off = [&](uint32_t t, uint32_t row_bytes, uint32_t col) __attribute__((always_inline)) {
+    return t < kv_rows ? t * row_bytes + col : 0x80000000u;
+  };
+  auto stage_flat = [&](int n, char* dst, const uint32_t (&tk)[kTokArr]) __attribute__((always_inline)) {
+    if constexpr (GATHER) {
+      char* const kb0 = const_cast<char*>(kbase);
+      char* const vb0 = const_cast<char*>(vbase);
+      if constexpr (INT8) {  // packed int8 keys: the step's rows as in the flat copy
+        int key0 = (n < 0 ? 0 : n) * BNS;
+        char* const kbs = kb0 + static_cast<uint64_t>(static_cast<uint32_t>(key0)) * krb;
+        const int knum = BNS * static_cast<int>(krb);
+#pragma unroll
+        for (int i = 0; i < C::KUPW; ++i)
+          buffer_copy16(kbs, knum, k_lo[i], dst + (wave * C::KUPW + i) * 1024);
+      } else {
+        const int knum = static_cast<int>(kv_rows * krb);
+#pragma unroll
+        for (int i = 0; i < C::KUPW; ++i)
+          buffer_copy16(kb0, knum, row_off(tk[i], krb, k_lo[i]),
+                        dst + (wave * C::KUPW + i) * 1024);
+      }
+      const int vnum = static_cast<int>(kv_rows * vrb);
+#pragma unroll
+      for (int i = 0; i < C::VUPW; ++i)
+        buffer_copy16(vb0, vnum, row_off(tk[i], vrb, v_lo[i]),
+                      dst + C::KBYTES + (wave * C::VUPW + i) * 1024);
+      return;
+    }
     int key0 = (n < 0 ? 0 : n) * BNS;
     key0 = key0 > klast ? klast : key0;
     const int left = klen - key0;  // >= 1
@@ -499,7 +568,8 @@ sparse_attn_kernel(AttnArgs a) {
   // later blocks once this block's QK MFMAs are issued (scalar loads return
   // out of order, so any LDS wait behind them waits for them too).
   auto compute = [&](const char* tile, int n, float kscale, uint64_t bits, int n_fill,
-                     char* fill, auto&& prefetch) __attribute__((always_inline)) {
+                     char* fill, const uint32_t (&fill_tok)[kTokArr],
+                     auto&& prefetch) __attribute__((always_inline)) {
     const uint64_t vmask = use_bits ? bits : __ballot(key_valid(n, tile));
     const bool all_valid = vmask == (~0ull >> (64 - C::HK));
     // ---- S^T = K Q^T: every K operand read is issued before the MFMAs ----
@@ -588,7 +658,7 @@ sparse_attn_kernel(AttnArgs a) {
     l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     if constexpr (kDmaInPv) {
       if constexpr (kValidCopy) stage_valid_flat(n_fill, fill);
-      stage_flat(n_fill, fill);
+      stage_flat(n_fill, fill, fill_tok);
     }
     // ---- O^T += V^T P^T, V^T operand by transposing LDS reads; the reads of
     //      the next 16-key step are in flight during this step's MFMAs ----
@@ -631,21 +701,35 @@ sparse_attn_kernel(AttnArgs a) {
   int n_m[3] = {-1, -1, -1};
   float ks_m[3] = {1.0f, 1.0f, 1.0f};
   uint2 mk_m[3] = {};  // raw validity words per slot (caller's bits only)
+  // slot-map entries of the step that fills each slot (GATHER)
+  uint32_t tk_m[3][kTokArr] = {};
+  int n_pre = -1;  // next step to stage
   if constexpr (kDmaInPv) {
     // both prologue steps always copy (step 0 stands in past the list), so
     // every wavefront has exactly 2 * kOps copies in flight
 #pragma unroll
     for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
-      char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
       n_m[sidx] = sidx < steps ? block_of(sidx) : -1;
       ks_m[sidx] = fetch_scale(n_m[sidx]);
+    }
+    if constexpr (GATHER) n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;
+    // gathered: the map reads go out one step ahead of their copies, in
+    // the order every ring iteration keeps (map j+1, copies j, map j+2, ...)
+    load_tokens(n_m[0], tk_m[0]);
+    load_tokens(n_m[1], tk_m[1]);
+#pragma unroll
+    for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
+      char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
       if constexpr (kValidCopy) stage_valid_flat(n_m[sidx], dst);
-      stage_flat(n_m[sidx], dst);
+      stage_flat(n_m[sidx], dst, tk_m[sidx]);
+      if (sidx == 0) load_tokens(n_pre, tk_m[2]);
     }
     if (use_bits) mk_m[0] = mask_words(n_m[0]);
-    // the Q loads precede these 2 * kOps copies: with at most that many
-    // outstanding, Q has landed and both prologue stages stay in flight
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOps));
+    if constexpr (!GATHER) n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;
+    // the Q loads (and the first two map reads) precede these 2 kOps copies
+    // (and the third map read): with at most that many outstanding, Q has
+    // landed and both prologue stages stay in flight
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kOps + kTok));
   } else {
 #pragma unroll
     for (int sidx = 0; sidx < STAGES - 1; ++sidx) {
@@ -657,8 +741,8 @@ sparse_attn_kernel(AttnArgs a) {
         stage(n_m[sidx], dst);
       }
     }
+    n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;
   }
-  int n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;  // next step to stage
   // 3-slot ring: the list entry of the step after n_pre, as loaded
   // (read only when the list is not empty: an empty list may have no entries)
   int32_t pre_raw =
@@ -675,7 +759,7 @@ sparse_attn_kernel(AttnArgs a) {
     // stages may remain (wavefront 0's extra validity copy is waited too),
     // then every wavefront's copies of block j have landed and slot F is free
     if constexpr (kDmaInPv) {
-      wait_vm_barrier<kOps>();  // every step issues kOps copies
+      wait_vm_barrier<kOps + kTok>();  // every step issues kOps copies (+ kTok map reads)
     } else if constexpr (STAGES == 3) {
       if (j + 1 < steps) wait_vm_barrier<C::DMA>();
       else wait_vm_barrier<0>();
@@ -697,10 +781,12 @@ sparse_attn_kernel(AttnArgs a) {
       n_pre = j + STAGES < steps ? block_step(pre_raw, j + STAGES) : -1;
       const int nxt = j + STAGES + 1 < steps ? j + STAGES + 1 : 0;  // in-bounds entry
       compute(tile, n_m[J], ks_m[J], use_bits ? mask_of(n_m[J], mk_m[J]) : 0ull, nf, fill,
-              [&]() __attribute__((always_inline)) {
+              tk_m[F], [&]() __attribute__((always_inline)) {
                 ks_m[F] = fetch_scale(nf);
                 pre_raw = ld_const(list + nxt / C::SUB);
                 if (use_bits) mk_m[N1] = mask_words(n_m[N1]);
+                // map entries of block j + 3, which will fill this block's slot
+                load_tokens(n_pre, tk_m[J]);
               });
     } else {
       if (j + STAGES - 1 < steps) {
@@ -710,7 +796,7 @@ sparse_attn_kernel(AttnArgs a) {
         stage(n_pre, fill);
         n_pre = j + STAGES < steps ? block_of(j + STAGES) : -1;
       }
-      compute(tile, n_m[J], ks_m[J], use_bits ? mask_bits(n_m[J]) : 0ull, -1, fill,
+      compute(tile, n_m[J], ks_m[J], use_bits ? mask_bits(n_m[J]) : 0ull, -1, fill, tk_m[F],
               []() __attribute__((always_inline)) {});
     }
   };
@@ -852,15 +938,23 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
     sparse_attn_kernel<INT8, D_, BM_, BN_, ST_, BN_, 2, false><<<grid, dim3(BM_ * 4), 0, s>>>(a); \
     return launch_status();                                                             \
   }
+  // gathered sources exist for the 3-slot rings with validity bits only
+  if (a.kv_tok != nullptr && !(a.kmask != nullptr && D == 128 && BM == 128 && BN == 128))
+    return RCSA_ERR_SHAPE;
   if constexpr (INT8) {  // the validity-bits flavour of the 3-slot ring
     if (a.kmask != nullptr && D == 128 && BM == 128 && BN == 128) {
-      sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true><<<grid, dim3(512), 0, s>>>(a);
+      if (a.kv_tok != nullptr)
+        sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true, true><<<grid, dim3(512), 0, s>>>(a);
+      else
+        sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true><<<grid, dim3(512), 0, s>>>(a);
       return launch_status();
     }
   }
   if constexpr (!INT8) {  // bf16 at D 128: a 3-slot ring of 64-key steps (3 x 32 KiB)
     if (D == 128 && BM == 128 && BN == 128) {
-      if (a.kmask != nullptr)
+      if (a.kv_tok != nullptr)
+        sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, true, true><<<grid, dim3(512), 0, s>>>(a);
+      else if (a.kmask != nullptr)
         sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, true><<<grid, dim3(512), 0, s>>>(a);
       else
         sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, false><<<grid, dim3(512), 0, s>>>(a);
@@ -1045,6 +1139,24 @@ static int fill_common(AttnArgs& a, const uint8_t* K_valid, float sm_scale, floa
   return RCSA_OK;
 }
 
+// Gathered V (and, with `gather_k`, K) rows: packed key slot s reads token row
+// kv_token[s] of a token-major source of kv_len rows (the strides given for
+// V/K are then token-major: row stride = token stride).  Needs the validity
+// bits and whole key blocks; the (b, h) plane of kv_len rows stays below 2^31
+// bytes so that an empty slot's offset lies past it.
+static int set_gather(AttnArgs& a, const int32_t* kv_token, int64_t kv_len, int64_t BN,
+                      bool gather_k) {
+  if (!kv_token) return RCSA_OK;
+  if (reinterpret_cast<uintptr_t>(kv_token) & 3u) return RCSA_ERR_ALIGN;
+  if (a.kmask == nullptr || kv_len <= 0 || a.k_len % BN != 0) return RCSA_ERR_SHAPE;
+  constexpr int64_t kPlane = int64_t{1} << 31;
+  if (kv_len * a.svn * 2 >= kPlane || (gather_k && kv_len * a.skn * 2 >= kPlane))
+    return RCSA_ERR_SHAPE;
+  a.kv_tok = kv_token;
+  a.kv_len = kv_len;
+  return RCSA_OK;
+}
+
 }  // namespace rcsa
 
 using namespace rcsa;
@@ -1059,7 +1171,8 @@ extern "C" int rcsa_sparse_attn_bf16_split(
     int64_t stride_bz, int64_t stride_bh, int64_t stride_bm, int64_t stride_lz,
     int64_t stride_lh, int64_t stride_lm, int64_t B, int64_t H, int64_t Q_LEN,
     int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N, int64_t max_k,
-    int64_t n_split, void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+    int64_t n_split, void* workspace, int64_t workspace_bytes, const int32_t* q_token,
+    int64_t q_tokens, const int32_t* kv_token, int64_t kv_len, hipStream_t stream) {
   if (!Q || !K || !V) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -1077,6 +1190,16 @@ extern "C" int rcsa_sparse_attn_bf16_split(
     a.kmask = K_block_mask;
     a.kvalid = nullptr;
   }
+  // gathered: Q rows in and O rows out through q_token, K/V rows through kv_token
+  if ((q_token == nullptr) != (kv_token == nullptr)) return RCSA_ERR_SHAPE;
+  if (q_token) {
+    if (reinterpret_cast<uintptr_t>(q_token) & 3u) return RCSA_ERR_ALIGN;
+    if (q_tokens <= 0 || q_tokens >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
+    a.out_tok = q_token;
+    a.out_len = q_tokens;
+  }
+  st = set_gather(a, kv_token, kv_len, BLOCK_N, true);
+  if (st) return st;
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
   if (a.n_items == 0) return RCSA_OK;
@@ -1095,7 +1218,8 @@ extern "C" int rcsa_sparse_attn_int8_split(
     int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
     int64_t BLOCK_N, int64_t max_k, int64_t n_split, void* workspace,
-    int64_t workspace_bytes, const int32_t* out_token, int64_t out_len, hipStream_t stream) {
+    int64_t workspace_bytes, const int32_t* out_token, int64_t out_len, const int32_t* kv_token,
+    int64_t kv_len, hipStream_t stream) {
   if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -1123,6 +1247,8 @@ extern "C" int rcsa_sparse_attn_int8_split(
     a.kmask = K_block_mask;
     a.kvalid = nullptr;
   }
+  st = set_gather(a, kv_token, kv_len, BLOCK_N, false);
+  if (st) return st;
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
   if (a.n_items == 0) return RCSA_OK;
@@ -1144,7 +1270,7 @@ extern "C" int rcsa_sparse_attn_int8_noalloc(
     int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
     int64_t BLOCK_N, int64_t max_k, int64_t n_split, const int32_t* out_token,
-    int64_t out_len, hipStream_t stream) {
+    int64_t out_len, const int32_t* kv_token, int64_t kv_len, hipStream_t stream) {
   if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -1172,6 +1298,8 @@ extern "C" int rcsa_sparse_attn_int8_noalloc(
     a.kmask = K_block_mask;
     a.kvalid = nullptr;
   }
+  st = set_gather(a, kv_token, kv_len, BLOCK_N, false);
+  if (st) return st;
   st = plan_split(a, n_split);
   if (st) return st;
   if (split_need(a, HEAD_DIM) > kScratchBytes) return RCSA_ERR_SCRATCH;
@@ -1203,7 +1331,8 @@ extern "C" int rcsa_sparse_attn_bf16(
       Q, K, V, K_valid, nullptr, sm_scale, M, Out, block_indices, block_indices_lens, stride_qz,
       stride_qh, stride_qm, stride_kz, stride_kh, stride_kn, stride_vz, stride_vh, stride_vn,
       stride_oz, stride_oh, stride_om, stride_bz, stride_bh, stride_bm, stride_lz, stride_lh,
-      stride_lm, B, H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, stream);
+      stride_lm, B, H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0,
+      nullptr, 0, nullptr, 0, stream);
 }
 
 extern "C" int rcsa_sparse_attn_int8(
@@ -1225,7 +1354,8 @@ extern "C" int rcsa_sparse_attn_int8(
       block_indices, block_indices_lens, stride_qz, stride_qh, stride_qm, stride_kz,
       stride_kh, stride_kn, stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
       stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B, H, Q_LEN, K_LEN,
-      HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, out_token, out_len, stream);
+      HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0, out_token, out_len, nullptr, 0,
+      stream);
 }
 
 extern "C" int64_t rcsa_attn_workspace_bytes(int64_t B, int64_t H, int64_t Q_LEN,

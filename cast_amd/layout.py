@@ -31,6 +31,7 @@ class CompactLayout:
     block_valid: torch.Tensor      # bool  [n_blocks, block_size]
     token_to_packed: torch.Tensor  # int64 [n_compact_tokens], packed slot of each token
     grid: tuple[int, int]          # (h tiles, w tiles)
+    slot_token32: torch.Tensor     # int32 [n_blocks * block_size], the kernels' slot map
 
     @property
     def slot_token(self) -> torch.Tensor:
@@ -88,7 +89,8 @@ def _compact_layout_cached(frames: tuple[int, ...], memory_temporal: int, height
     nh = math.ceil(height / block_shape[1])
     nw = math.ceil(width / block_shape[2])
     return CompactLayout(block_shape, n_blocks, bs, block_indices, block_indices >= 0,
-                         token_to_packed, (nh, nw))
+                         token_to_packed, (nh, nw),
+                         block_indices.reshape(-1).to(torch.int32).contiguous())
 
 
 def compact_layout(active_frames: Sequence[int], memory_temporal: int, height: int,

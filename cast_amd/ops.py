@@ -149,11 +149,13 @@ def _tokens_bhld(x: torch.Tensor, slots: torch.Tensor, block_size: int, fn: str)
 def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Tensor,
                    k_valid: Optional[torch.Tensor], block_size: int, *,
                    q_slot_token: Optional[torch.Tensor] = None,
-                   k_slot_token: Optional[torch.Tensor] = None):
+                   k_slot_token: Optional[torch.Tensor] = None, quantize: bool = True):
     """``pool_query(q, q_valid, quantize=True)`` and ``pool_key(k, k_valid, stats=True,
     block_mask=True)`` in one launch (no reference counterpart: the int8 layer call's
     pooling pass).  Returns ``(qhat, q_i8, q_scale, khat, ksum, kmin, kmax, block_mask)``,
-    bit for bit the two calls' outputs.
+    bit for bit the two calls' outputs.  ``quantize=False`` drops the query
+    quantiser and the key statistics (those five outputs are None): the bf16
+    path's pass.
 
     With ``q_slot_token`` / ``k_slot_token`` (both or neither) q and k are token-major
     ``[B, L, H, D]`` sources gathered on the fly: the outputs equal those of
@@ -187,15 +189,19 @@ def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Te
     kv = _valid_u8(k_valid, Lk, k.device, fn)
     f32 = dict(device=q.device, dtype=torch.float32)
     qhat = torch.empty(B * H, NQ, D, **f32)
-    q_i8 = torch.empty(B, H, Lq, D, device=q.device, dtype=torch.int8)
-    q_scale = torch.empty(B * H, NQ, **f32)
-    khat, ksum, kmin, kmax = (torch.empty(B * H, NK, D, **f32) for _ in range(4))
+    khat = torch.empty(B * H, NK, D, **f32)
+    if quantize:
+        q_i8 = torch.empty(B, H, Lq, D, device=q.device, dtype=torch.int8)
+        q_scale = torch.empty(B * H, NQ, **f32)
+        ksum, kmin, kmax = (torch.empty(B * H, NK, D, **f32) for _ in range(3))
+    else:
+        q_i8 = q_scale = ksum = kmin = kmax = None
     mask = torch.empty(NK, block_size // 32, device=k.device, dtype=torch.int32)
     st = _lib.load().rcsa_pool_query_key(
         q.data_ptr(), k.data_ptr(), code, B, H, NQ, NK, block_size, D, *q_strides, *k_strides,
         _ptr(qv), _ptr(kv), _ptr(qm), q_src, _ptr(km), k_src,
-        qhat.data_ptr(), q_i8.data_ptr(), q_scale.data_ptr(),
-        khat.data_ptr(), ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), mask.data_ptr(),
+        qhat.data_ptr(), _ptr(q_i8), _ptr(q_scale),
+        khat.data_ptr(), _ptr(ksum), _ptr(kmin), _ptr(kmax), mask.data_ptr(),
         _stream())
     check(st, fn)
     return qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask
@@ -498,9 +504,15 @@ def _check_block_mask(block_mask, Lk, block_n, device, fn):
     return block_mask.contiguous()
 
 
+def _bhld_strides(x: torch.Tensor, token_major: bool):
+    """(stride_b, stride_h, stride_row) of [B, H, L, D] or token-major [B, L, H, D]."""
+    return ((x.stride(0), x.stride(2), x.stride(1)) if token_major
+            else (x.stride(0), x.stride(1), x.stride(2)))
+
+
 def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block_n=128,
                      sm_scale=None, return_lse=False, out=None, n_split=None,
-                     block_mask=None):
+                     block_mask=None, q_token=None, kv_token=None):
     """bf16 block-sparse attention; the ``_attn_fwd_bsa_align`` contract.
 
     q/k/v [B, H, L, D] bf16, indices int32 [B|1, H|1, NQB, maxK], counts
@@ -509,43 +521,71 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
     replaces ``valid`` when given.
     ``n_split`` splits every block list over that many workgroups (merged
     afterwards); None picks it from the device's compute-unit count.
+
+    ``q_token`` / ``kv_token`` (slot -> token maps of the packed query and key
+    slots, both or neither; needs ``block_mask``, D 128, 128-token blocks):
+    q is token-major ``[B, Lq_tokens, H, D]`` and k, v ``[B, Lk_tokens, H, D]``;
+    the kernel reads their rows through the maps (the q[:, flat] / k[:, flat] /
+    v[:, flat] packing of P/matrix_curvature_phase_frame_weave.py:5677-5684)
+    and writes the output (and LSE) to the token rows, ``[B, Lq_tokens, H, D]``
+    (P/matrix_curvature_phase_frame_weave.py:6095).  Empty slots read zeros.
     """
     fn = "sparse_attn_bf16"
     _require_cuda(fn, q, k, v, indices, counts)
     _attn_common(q, k, v, indices, counts, fn)
     if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
         raise TypeError(f"{fn}: q/k/v must be bfloat16")
-    B, H, Lq, D = q.shape
-    Lk = k.shape[2]
-    if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
-        raise ValueError(f"{fn}: k/v shape mismatch")
+    if (q_token is None) != (kv_token is None):
+        raise ValueError(f"{fn}: give both slot maps or neither")
+    gathered = q_token is not None
+    if gathered:
+        if block_mask is None:
+            raise ValueError(f"{fn}: gathered sources need block_mask")
+        qm = _slot_map(q_token, block_m, q.device, fn)
+        km = _slot_map(kv_token, block_n, q.device, fn)
+        B, n_qtok, H, D = q.shape
+        n_ktok = k.shape[1]
+        Lq, Lk = qm.numel(), km.numel()
+        if k.shape != (B, n_ktok, H, D) or v.shape != (B, n_ktok, H, D):
+            raise ValueError(f"{fn}: k/v must be token-major [B, Lk_tokens, H, D] alike")
+    else:
+        qm = km = None
+        n_qtok = n_ktok = 0
+        B, H, Lq, D = q.shape
+        Lk = k.shape[2]
+        if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
+            raise ValueError(f"{fn}: k/v shape mismatch")
     indices, counts = _expand_lists(indices, counts, B, H)
     if block_mask is not None:
         block_mask = _check_block_mask(block_mask, Lk, block_n, q.device, fn)
         kv = None
     else:
         kv = _valid_u8(valid, Lk, q.device, fn)
+    n_rows = n_qtok if gathered else Lq
     if out is None:
-        out = torch.empty_like(q, memory_format=torch.contiguous_format)
-    lse = torch.empty(B, H, Lq, device=q.device, dtype=torch.float32) if return_lse else None
+        out = (torch.empty(B, n_qtok, H, D, device=q.device, dtype=torch.bfloat16) if gathered
+               else torch.empty_like(q, memory_format=torch.contiguous_format))
+    lse = torch.empty(B, H, n_rows, device=q.device, dtype=torch.float32) if return_lse else None
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q.device, fn)
     st = _lib.load().rcsa_sparse_attn_bf16_split(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(kv), _ptr(block_mask), scale, _ptr(lse),
         out.data_ptr(),
         indices.data_ptr(), counts.data_ptr(),
-        q.stride(0), q.stride(1), q.stride(2), k.stride(0), k.stride(1), k.stride(2),
-        v.stride(0), v.stride(1), v.stride(2), out.stride(0), out.stride(1), out.stride(2),
+        *_bhld_strides(q, gathered), *_bhld_strides(k, gathered), *_bhld_strides(v, gathered),
+        *_bhld_strides(out, gathered),
         indices.stride(0), indices.stride(1), indices.stride(2),
         counts.stride(0), counts.stride(1), counts.stride(2),
-        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _stream())
+        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes,
+        _ptr(qm), n_qtok, _ptr(km), n_ktok, _stream())
     check(st, fn)
     return (out, lse) if return_lse else out
 
 
 def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=None, *,
                      block_m=128, block_n=128, sm_scale=None, return_lse=False, out=None,
-                     n_split=None, block_mask=None, out_token=None, out_len=None):
+                     n_split=None, block_mask=None, out_token=None, out_len=None,
+                     v_token=None):
     """int8-QK / bf16-PV block-sparse attention over quantiser outputs.
 
     ``block_mask`` (int32 ``[ceil(Lk / block_n), block_n // 32]``, e.g. from
@@ -553,7 +593,11 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
     replaces ``valid``.  ``out_token`` (a slot -> token map of the packed queries)
     scatters the output into a token-major ``[B, out_len, H, D]`` tensor (and the
     LSE into ``[B, H, out_len]``): ``unpack_tokens`` fused into the epilogue
-    (P/matrix_curvature_phase_frame_weave.py:6095).  Every token must own a slot."""
+    (P/matrix_curvature_phase_frame_weave.py:6095).  Every token must own a slot.
+    ``v_token`` (a slot -> token map of the packed keys; needs ``block_mask``,
+    D 128, 128-token blocks) reads V rows from a token-major ``[B, Lv_tokens, H, D]``
+    v through the map inside the attention's copy ring (the v[:, flat] packing
+    of P/matrix_curvature_phase_frame_weave.py:5677-5684); empty slots read zeros."""
     fn = "sparse_attn_int8"
     _require_cuda(fn, q_i8, q_scale, k_i8, k_scale, v, indices, counts)
     _attn_common(q_i8, k_i8, v, indices, counts, fn)
@@ -561,8 +605,19 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         raise TypeError(f"{fn}: q/k must be int8 and v bfloat16")
     B, H, Lq, D = q_i8.shape
     Lk = k_i8.shape[2]
-    if k_i8.shape != (B, H, Lk, D) or v.shape[:2] != (B, H) or v.shape[3] != D \
-            or v.shape[2] < Lk:
+    if v_token is not None:
+        if block_mask is None:
+            raise ValueError(f"{fn}: a gathered V needs block_mask")
+        vm = _slot_map(v_token, block_n, q_i8.device, fn)
+        if vm.numel() != Lk or v.ndim != 4 or v.shape[0] != B or v.shape[2:] != (H, D):
+            raise ValueError(f"{fn}: v_token needs {Lk} slots and v [B, Lv_tokens, H, D]")
+        v_rows = v.shape[1]
+        v_strides = _bhld_strides(v, True)
+    else:
+        vm, v_rows = None, 0
+        v_strides = _bhld_strides(v, False)
+    if k_i8.shape != (B, H, Lk, D) or (vm is None and (
+            v.shape[:2] != (B, H) or v.shape[3] != D or v.shape[2] < Lk)):
         raise ValueError(f"{fn}: k/v shape mismatch")
     nqb = -(-Lq // block_m)
     nkb = -(-Lk // block_n)
@@ -603,12 +658,11 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
         scale, _ptr(lse),
         out.data_ptr(), indices.data_ptr(), counts.data_ptr(),
         q_i8.stride(0), q_i8.stride(1), q_i8.stride(2),
-        k_i8.stride(0), k_i8.stride(1), k_i8.stride(2),
-        v.stride(0), v.stride(1), v.stride(2), *o_strides,
+        k_i8.stride(0), k_i8.stride(1), k_i8.stride(2), *v_strides, *o_strides,
         indices.stride(0), indices.stride(1), indices.stride(2),
         counts.stride(0), counts.stride(1), counts.stride(2),
         B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _ptr(om),
-        n_out, _stream())
+        n_out, _ptr(vm), v_rows, _stream())
     check(st, fn)
     return (out, lse) if return_lse else out
 

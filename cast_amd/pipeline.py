@@ -74,23 +74,34 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ``overlap`` runs the scores and the top-k on a side stream beside the
     int8 key pass.  Results are identical either way.
 
-    ``q_slot_token`` / ``k_slot_token`` (int8 only, both or neither; e.g. a
+    ``q_slot_token`` / ``k_slot_token`` (both or neither; e.g. a
     ``CompactLayout.slot_token``): q, k and v are token-major ``[B, L, H, D]``
-    and the packing happens inside the kernels.  The pooling pass and the key
-    quantiser gather Q/K rows through the maps, V is packed once, and the
-    attention writes its output (and LSE) straight to the token rows, so
-    ``out`` is ``[B, Lq_tokens, H, D]``.  The results equal those of the packed
-    call on ``pack_tokens`` inputs followed by ``unpack_tokens``.
+    and the packing happens inside the kernels.  The pooling pass (and the
+    int8 key quantiser) gather Q/K rows through the maps, the attention's copy
+    ring gathers V (bf16: also K, and Q rows) through them, and the attention
+    writes its output (and LSE) straight to the token rows, so ``out`` is
+    ``[B, Lq_tokens, H, D]``.  The results equal those of the packed call on
+    ``pack_tokens`` inputs followed by ``unpack_tokens``.  (D 128 and 128-token
+    blocks; other shapes pack V first.)
     """
     gathered = q_slot_token is not None or k_slot_token is not None
+    v_token = None
     if gathered:
         if q_slot_token is None or k_slot_token is None:
             raise ValueError("rcsa_attention: give both slot maps or neither")
-        if not int8:
-            raise ValueError("rcsa_attention: gathered inputs need the int8 path")
         B, _, H, D = q.shape
+        dev = q.device
+        q_slot_token = q_slot_token.to(device=dev, dtype=torch.int32).contiguous()
+        k_slot_token = k_slot_token.to(device=dev, dtype=torch.int32).contiguous()
         Lq, Lk = q_slot_token.numel(), k_slot_token.numel()
-        v = ops.pack_tokens(v, k_slot_token)  # V is read by the attention only
+        ring_gather = D == 128 and block_size == 128 and v.dtype == torch.bfloat16
+        if not int8 and not ring_gather:
+            raise ValueError("rcsa_attention: gathered bf16 inputs need D 128, "
+                             "128-token blocks and bf16 sources")
+        if ring_gather:
+            v_token = k_slot_token  # V rows are read through the map by the attention
+        else:
+            v = ops.pack_tokens(v, k_slot_token)
     else:
         B, H, Lq, D = q.shape
         Lk = k.shape[2]
@@ -108,6 +119,10 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     if int8:  # one launch pools Q (+ int8) and K (+ stats and validity bits)
         qhat, q_i8, q_scale, khat, ksum, kmin, kmax, k_mask = ops.pool_query_key(
             q, q_valid, k, k_valid, bs, q_slot_token=q_slot_token, k_slot_token=k_slot_token)
+    elif gathered:  # bf16: pooled blocks and validity bits, through the maps
+        qhat, q_i8, q_scale, khat, ksum, kmin, kmax, k_mask = ops.pool_query_key(
+            q, q_valid, k, k_valid, bs, q_slot_token=q_slot_token, k_slot_token=k_slot_token,
+            quantize=False)
     else:  # the bf16 attention takes the key validity as bits from the key pooling pass
         qhat, q_i8, q_scale = ops.pool_query(q, q_valid, bs)
         khat, ksum, kmin, kmax, k_mask = ops.pool_key(k, k_valid, bs, block_mask=True)
@@ -149,7 +164,7 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                                    block_m=bs, block_n=bs, sm_scale=scale,
                                    return_lse=return_lse, n_split=n_split, block_mask=k_mask,
                                    out_token=q_slot_token if gathered else None,
-                                   out_len=q.shape[1] if gathered else None)
+                                   out_len=q.shape[1] if gathered else None, v_token=v_token)
     else:
         k_i8 = k_scale = kmean = None
         qb = q if q.dtype == torch.bfloat16 else q.to(torch.bfloat16)
@@ -157,7 +172,9 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         vb = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
         res = ops.sparse_attn_bf16(qb, kb, vb, idx4, cnt3, None, block_m=bs, block_n=bs,
                                    sm_scale=scale, return_lse=return_lse, n_split=n_split,
-                                   block_mask=k_mask)
+                                   block_mask=k_mask,
+                                   q_token=q_slot_token if gathered else None,
+                                   kv_token=k_slot_token if gathered else None)
     out, lse = res if return_lse else (res, None)
     return RCSAResult(out, idx4, cnt3, score, qhat, khat, lse, q_i8, q_scale, k_i8, k_scale,
                       kmean, k_mask)

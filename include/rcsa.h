@@ -110,6 +110,10 @@ int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_heads,
  * ungathered call, bit for bit, without the packed copies.  Fuses the
  * q[:, flat] / k[:, flat] gathers of P/matrix_curvature_phase_frame_weave.py:5677-5684
  * into the pooling pass; q_valid / k_valid, when given, stay per packed slot.
+ *
+ * q_i8, q_scale, ksum, kmin and kmax may all be NULL together: then only the
+ * pooled blocks (and block_mask) are written — rcsa_pool_query without the
+ * quantiser and rcsa_pool_key without the statistics, the bf16 path's pass.
  */
 int rcsa_pool_query_key(const void* q, const void* k, int dtype, int64_t batch,
                         int64_t n_heads, int64_t n_qblocks, int64_t n_kblocks,
@@ -334,6 +338,20 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
  * word w of block n = validity of key n * BLOCK_N + 32 w + i, 4-byte aligned,
  * as rcsa_pool_key writes it); when it is not NULL the bits replace K_valid.
  * workspace: 16-byte aligned, at least rcsa_attn_workspace_bytes(...) bytes.
+ *
+ * Gathered sources (the q[:, flat] / k[:, flat] / v[:, flat] gathers and the
+ * scatter back to token rows of P/matrix_curvature_phase_frame_weave.py:
+ * 5677-5684 and 6095 fused into the kernel; no reference counterpart as an
+ * entry point).  kv_token (int32 [K_LEN], 4-byte aligned; NULL = packed
+ * sources) maps packed key slot s to row kv_token[s] of a token-major V
+ * ([B, kv_len, H, D]; stride_vn is then the token stride) — for the bf16
+ * variant also of K — and -1 (or a row >= kv_len) is an empty slot that reads
+ * zeros.  The bf16 variant takes q_token (int32 [Q_LEN]) with it: Q row r is
+ * token q_token[r] of a token-major Q of q_tokens rows, and O / M are written
+ * to that token row ([B, q_tokens, H, D] / [B, H, q_tokens]; -1 rows are
+ * dropped), as out_token does for the int8 variant.  Needs K_block_mask,
+ * HEAD_DIM 128, BLOCK_M = BLOCK_N = 128, K_LEN a multiple of 128 and
+ * kv_len x (V, bf16 also K) row stride below 2^31 bytes; else RCSA_ERR_SHAPE.
  */
 int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
                                 const uint8_t* K_valid, const uint32_t* K_block_mask,
@@ -349,7 +367,9 @@ int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
                                 int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
                                 int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
                                 int64_t max_k, int64_t n_split, void* workspace,
-                                int64_t workspace_bytes, hipStream_t stream);
+                                int64_t workspace_bytes, const int32_t* q_token,
+                                int64_t q_tokens, const int32_t* kv_token, int64_t kv_len,
+                                hipStream_t stream);
 int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t q_scale_stride, const int8_t* K,
                                 const float* k_scale, int64_t k_scale_stride,
@@ -367,7 +387,8 @@ int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
                                 int64_t max_k, int64_t n_split, void* workspace,
                                 int64_t workspace_bytes, const int32_t* out_token,
-                                int64_t out_len, hipStream_t stream);
+                                int64_t out_len, const int32_t* kv_token, int64_t kv_len,
+                                hipStream_t stream);
 
 /*
  * The split int8 entry point with no workspace argument: it allocates
@@ -398,7 +419,8 @@ int rcsa_sparse_attn_int8_noalloc(const int8_t* Q, const float* q_scale,
                                   int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN,
                                   int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N,
                                   int64_t max_k, int64_t n_split, const int32_t* out_token,
-                                  int64_t out_len, hipStream_t stream);
+                                  int64_t out_len, const int32_t* kv_token, int64_t kv_len,
+                                  hipStream_t stream);
 
 /* Size in bytes of the static scratch of rcsa_sparse_attn_int8_noalloc. */
 int64_t rcsa_attn_noalloc_scratch_bytes(void);

@@ -58,8 +58,104 @@ def test_gathered_pooling_and_quantiser_match_packed(dtype):
     assert int(qk_got[0][:, :, empty].abs().sum()) == 0
 
 
+def test_gathered_pooling_without_quantiser_matches_packed():
+    """The bf16 path's pass: pooled blocks and validity bits only."""
+    from cast_amd import ops
+    lay_q, lay_k, q, k, v = _case(seed=8)
+    print("gather pooling, no quantiser", flush=True)
+    qhat, _, _ = ops.pool_query(_packed(q, lay_q), lay_q.slot_valid, 128)
+    khat, _, _, _, mask = ops.pool_key(_packed(k, lay_k), lay_k.slot_valid, 128,
+                                       block_mask=True)
+    got = ops.pool_query_key(q, None, k, None, 128, q_slot_token=lay_q.slot_token32,
+                             k_slot_token=lay_k.slot_token32, quantize=False)
+    assert all(got[i] is None for i in (1, 2, 4, 5, 6))
+    assert torch.equal(got[0], qhat) and torch.equal(got[3], khat) and torch.equal(got[7], mask)
+
+
+def _holey_map(n_tokens, n_slots, g, dev):
+    """A slot -> token map over n_slots slots: a random permutation of the
+    tokens with every fifth slot empty (-1) and one slot past the tokens."""
+    m = torch.full((n_slots,), -1, dtype=torch.int32)
+    keep = torch.arange(n_slots) % 5 != 4
+    perm = torch.randperm(n_tokens, generator=g)[:int(keep.sum())]
+    m[keep] = perm.int()
+    m[7] = n_tokens + 3  # a row past the source: empty as well
+    return m.to(dev)
+
+
 @pytest.mark.parametrize("n_split", [1, 3])
-def test_gathered_layer_call_matches_pack_unpack(n_split):
+def test_int8_attention_reads_v_through_map(n_split):
+    """sparse_attn_int8 with v_token (V rows gathered in the copy ring) equals
+    the call on the packed V, bit for bit."""
+    from cast_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(21 + n_split)
+    B, H, D, nqb, nkb, max_k, n_tok = 1, 6, 128, 20, 24, 10, 2600
+    q8 = torch.randint(-127, 128, (B, H, nqb * 128, D), generator=g, dtype=torch.int8).to(dev)
+    k8 = torch.randint(-127, 128, (B, H, nkb * 128, D), generator=g, dtype=torch.int8).to(dev)
+    qs = (torch.rand(B * H, nqb, generator=g) * 1e-3 + 1e-4).to(dev)
+    ks = (torch.rand(B * H, nkb, generator=g) * 1e-3 + 1e-4).to(dev)
+    v_tok = (torch.randn(B, n_tok, H, D, generator=g)).bfloat16().to(dev)
+    vmap = _holey_map(n_tok, nkb * 128, g, dev)
+    v_packed = ops.pack_tokens(v_tok, vmap)
+    valid = (vmap >= 0) & (vmap < n_tok)
+    # the validity bits of the packed keys, as the pooling pass writes them
+    mask = ops.pool_key(v_packed, valid, 128, block_mask=True)[4]
+    idx = torch.stack([torch.randperm(nkb, generator=g)[:max_k].sort().values
+                       for _ in range(B * H * nqb)]).reshape(B, H, nqb, max_k).int().to(dev)
+    cnt = torch.randint(1, max_k + 1, (B, H, nqb), generator=g, dtype=torch.int32).to(dev)
+    print(f"int8 v_token n_split {n_split}", flush=True)
+    want, lse_w = ops.sparse_attn_int8(q8, qs, k8, ks, v_packed, idx, cnt, None, block_mask=mask,
+                                       return_lse=True, n_split=n_split)
+    got, lse_g = ops.sparse_attn_int8(q8, qs, k8, ks, v_tok, idx, cnt, None, block_mask=mask,
+                                      return_lse=True, n_split=n_split, v_token=vmap)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want) and torch.equal(lse_g, lse_w)
+    with pytest.raises(ValueError):  # the gathered V rides with the validity bits only
+        ops.sparse_attn_int8(q8, qs, k8, ks, v_tok, idx, cnt, None, v_token=vmap)
+
+
+@pytest.mark.parametrize("n_split", [1, 3])
+def test_bf16_attention_reads_rows_through_maps(n_split):
+    """sparse_attn_bf16 with q_token / kv_token equals the call on packed
+    inputs followed by the unpack of its output, bit for bit."""
+    from cast_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(31 + n_split)
+    B, H, D, nqb, nkb, max_k = 1, 4, 128, 12, 20, 9
+    nq_tok, nk_tok = nqb * 128 - 100, 2400
+    q_tok = (torch.randn(B, nq_tok, H, D, generator=g) / D ** 0.5).bfloat16().to(dev)
+    k_tok = (torch.randn(B, nk_tok, H, D, generator=g) / D ** 0.5).bfloat16().to(dev)
+    v_tok = torch.randn(B, nk_tok, H, D, generator=g).bfloat16().to(dev)
+    # every query token owns exactly one slot (the output is written through the map)
+    qmap = torch.full((nqb * 128,), -1, dtype=torch.int32)
+    qslots = torch.randperm(nqb * 128, generator=g)[:nq_tok]
+    qmap[qslots] = torch.arange(nq_tok, dtype=torch.int32)
+    qmap = qmap.to(dev)
+    kmap = _holey_map(nk_tok, nkb * 128, g, dev)
+    kvalid = ((kmap >= 0) & (kmap < nk_tok))
+    _, _, _, _, mask = ops.pool_key(ops.pack_tokens(k_tok, kmap), kvalid, 128, block_mask=True)
+    idx = torch.stack([torch.randperm(nkb, generator=g)[:max_k].sort().values
+                       for _ in range(B * H * nqb)]).reshape(B, H, nqb, max_k).int().to(dev)
+    cnt = torch.randint(1, max_k + 1, (B, H, nqb), generator=g, dtype=torch.int32).to(dev)
+    print(f"bf16 q_token/kv_token n_split {n_split}", flush=True)
+    want, lse_w = ops.sparse_attn_bf16(ops.pack_tokens(q_tok, qmap), ops.pack_tokens(k_tok, kmap),
+                                       ops.pack_tokens(v_tok, kmap), idx, cnt, None,
+                                       block_mask=mask, return_lse=True, n_split=n_split)
+    got, lse_g = ops.sparse_attn_bf16(q_tok, k_tok, v_tok, idx, cnt, None, block_mask=mask,
+                                      return_lse=True, n_split=n_split, q_token=qmap,
+                                      kv_token=kmap)
+    torch.cuda.synchronize()
+    t2p = torch.empty(nq_tok, dtype=torch.long, device=dev)
+    t2p[qmap[qslots.to(dev)].long()] = qslots.to(dev)
+    assert got.shape == (B, nq_tok, H, D)
+    assert torch.equal(got, ops.unpack_tokens(want, t2p))
+    assert torch.equal(lse_g, lse_w[:, :, t2p])
+
+
+@pytest.mark.parametrize("int8", [True, False])
+@pytest.mark.parametrize("n_split", [1, 3])
+def test_gathered_layer_call_matches_pack_unpack(n_split, int8):
     from cast_amd import ops
     from cast_amd.pipeline import rcsa_attention
     lay_q, lay_k, q, k, v = _case(seed=6)
@@ -67,13 +163,14 @@ def test_gathered_layer_call_matches_pack_unpack(n_split):
     forced = torch.zeros(nq, nk, dtype=torch.bool)
     forced[:, nk - 30:] = True  # the current frames' blocks are always kept
     k_select = 30 + 16
-    print(f"gather layer call n_split {n_split} q blocks {nq} k blocks {nk}", flush=True)
+    print(f"gather layer call int8 {int8} n_split {n_split} q blocks {nq} k blocks {nk}",
+          flush=True)
     ref = rcsa_attention(_packed(q, lay_q), _packed(k, lay_k), _packed(v, lay_k),
                          lay_q.slot_valid, lay_k.slot_valid, block_size=128, k_select=k_select,
-                         forced=forced, int8=True, max_k=k_select, return_lse=True,
+                         forced=forced, int8=int8, max_k=k_select, return_lse=True,
                          n_split=n_split)
     got = rcsa_attention(q, k, v, None, None, block_size=128, k_select=k_select,
-                         forced=forced, int8=True, max_k=k_select, return_lse=True,
+                         forced=forced, int8=int8, max_k=k_select, return_lse=True,
                          n_split=n_split, q_slot_token=lay_q.slot_token,
                          k_slot_token=lay_k.slot_token)
     torch.cuda.synchronize()
