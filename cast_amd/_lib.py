@@ -41,7 +41,7 @@ SIGNATURES: dict[str, list] = {
     "rcsa_sparse_attn_int8": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P, _P]
                              + [_I] * 18 + [_I] * 8 + [_P, _I, _P],
     "rcsa_sparse_attn_bf16_split": [_P, _P, _P, _P, _P, c_float, _P, _P, _P, _P] + [_I] * 18
-                                   + [_I] * 8 + [_I, _P, _I, _P, _I, _P, _I, _P],
+                                   + [_I] * 8 + [_I, _P, _I, _P, _I, _P, _I, _P, _I, _P],
     "rcsa_sparse_attn_int8_split": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P, _P]
                                    + [_I] * 18 + [_I] * 8 + [_I, _P, _I, _P, _I, _P, _I, _P],
     "rcsa_sparse_attn_int8_noalloc": [_P, _P, _I, _P, _P, _I, _P, _P, _P, c_float, _P, _P, _P,

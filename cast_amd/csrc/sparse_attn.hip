@@ -74,10 +74,12 @@ struct AttnArgs {
   int64_t out_len;
   // Gathered sources (GATHER kernels only): packed key slot s reads row
   // kv_tok[s] of a token-major V (and, bf16, K) with kv_len token rows; -1
-  // or a row >= kv_len is an empty slot (zeros).  bf16 Q rows come through
-  // out_tok (the same query map the output is written through).
+  // or a row >= kv_len is an empty slot (zeros).  bf16 query row r reads row
+  // q_tok[r] of a token-major Q of q_src_len rows (zeros when empty).
   const int32_t* kv_tok;
   int64_t kv_len;
+  const int32_t* q_tok;
+  int64_t q_src_len;
 };
 
 // Output row of packed query row r, or -1 when the row is not written.
@@ -289,8 +291,8 @@ sparse_attn_kernel(AttnArgs a) {
   bool qrow_ok = qrow < a.q_len;
   int64_t qsrc = qrow;  // source row of the Q load
   if constexpr (GATHER && !INT8) {  // bf16 queries are read through the query map
-    const int32_t t = qrow_ok ? a.out_tok[qrow] : -1;
-    qrow_ok = t >= 0 && t < a.out_len;
+    const int32_t t = qrow_ok ? a.q_tok[qrow] : -1;
+    qrow_ok = t >= 0 && t < a.q_src_len;
     qsrc = t;
   }
 
@@ -1172,7 +1174,8 @@ extern "C" int rcsa_sparse_attn_bf16_split(
     int64_t stride_lh, int64_t stride_lm, int64_t B, int64_t H, int64_t Q_LEN,
     int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M, int64_t BLOCK_N, int64_t max_k,
     int64_t n_split, void* workspace, int64_t workspace_bytes, const int32_t* q_token,
-    int64_t q_tokens, const int32_t* kv_token, int64_t kv_len, hipStream_t stream) {
+    int64_t q_tokens, const int32_t* kv_token, int64_t kv_len, const int32_t* out_token,
+    int64_t out_len, hipStream_t stream) {
   if (!Q || !K || !V) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
@@ -1190,13 +1193,20 @@ extern "C" int rcsa_sparse_attn_bf16_split(
     a.kmask = K_block_mask;
     a.kvalid = nullptr;
   }
-  // gathered: Q rows in and O rows out through q_token, K/V rows through kv_token
+  // gathered: Q rows through q_token, K/V rows through kv_token, O rows out
+  // through out_token (or, when it is NULL, through q_token)
   if ((q_token == nullptr) != (kv_token == nullptr)) return RCSA_ERR_SHAPE;
+  if (out_token && !q_token) return RCSA_ERR_SHAPE;
   if (q_token) {
-    if (reinterpret_cast<uintptr_t>(q_token) & 3u) return RCSA_ERR_ALIGN;
+    if ((reinterpret_cast<uintptr_t>(q_token) & 3u) ||
+        (reinterpret_cast<uintptr_t>(out_token) & 3u))
+      return RCSA_ERR_ALIGN;
     if (q_tokens <= 0 || q_tokens >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
-    a.out_tok = q_token;
-    a.out_len = q_tokens;
+    if (out_token && (out_len <= 0 || out_len >= (int64_t{1} << 31))) return RCSA_ERR_SHAPE;
+    a.q_tok = q_token;
+    a.q_src_len = q_tokens;
+    a.out_tok = out_token ? out_token : q_token;
+    a.out_len = out_token ? out_len : q_tokens;
   }
   st = set_gather(a, kv_token, kv_len, BLOCK_N, true);
   if (st) return st;
@@ -1332,7 +1342,7 @@ extern "C" int rcsa_sparse_attn_bf16(
       stride_qh, stride_qm, stride_kz, stride_kh, stride_kn, stride_vz, stride_vh, stride_vn,
       stride_oz, stride_oh, stride_om, stride_bz, stride_bh, stride_bm, stride_lz, stride_lh,
       stride_lm, B, H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 1, nullptr, 0,
-      nullptr, 0, nullptr, 0, stream);
+      nullptr, 0, nullptr, 0, nullptr, 0, stream);
 }
 
 extern "C" int rcsa_sparse_attn_int8(

@@ -512,7 +512,8 @@ def _bhld_strides(x: torch.Tensor, token_major: bool):
 
 def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block_n=128,
                      sm_scale=None, return_lse=False, out=None, n_split=None,
-                     block_mask=None, q_token=None, kv_token=None):
+                     block_mask=None, q_token=None, kv_token=None, out_token=None,
+                     out_len=None):
     """bf16 block-sparse attention; the ``_attn_fwd_bsa_align`` contract.
 
     q/k/v [B, H, L, D] bf16, indices int32 [B|1, H|1, NQB, maxK], counts
@@ -529,6 +530,9 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
     v[:, flat] packing of P/matrix_curvature_phase_frame_weave.py:5677-5684)
     and writes the output (and LSE) to the token rows, ``[B, Lq_tokens, H, D]``
     (P/matrix_curvature_phase_frame_weave.py:6095).  Empty slots read zeros.
+    ``out_token`` / ``out_len`` (with the maps) write output row r to row
+    ``out_token[r]`` of ``[B, out_len, H, D]`` instead, e.g. a relay layer's
+    query-frame rows (P/matrix_curvature_phase_frame_weave.py:8990-8994).
     """
     fn = "sparse_attn_bf16"
     _require_cuda(fn, q, k, v, indices, counts)
@@ -548,9 +552,18 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
         Lq, Lk = qm.numel(), km.numel()
         if k.shape != (B, n_ktok, H, D) or v.shape != (B, n_ktok, H, D):
             raise ValueError(f"{fn}: k/v must be token-major [B, Lk_tokens, H, D] alike")
+        if out_token is not None:
+            om = _slot_map(out_token, block_m, q.device, fn)
+            if om.numel() != Lq or out_len is None or int(out_len) <= 0:
+                raise ValueError(f"{fn}: out_token needs {Lq} slots and a positive out_len")
+            n_out = int(out_len)
+        else:
+            om, n_out = None, n_qtok
     else:
-        qm = km = None
-        n_qtok = n_ktok = 0
+        if out_token is not None:
+            raise ValueError(f"{fn}: out_token needs the gathered form")
+        qm = km = om = None
+        n_qtok = n_ktok = n_out = 0
         B, H, Lq, D = q.shape
         Lk = k.shape[2]
         if k.shape != (B, H, Lk, D) or v.shape != (B, H, Lk, D):
@@ -561,10 +574,12 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
         kv = None
     else:
         kv = _valid_u8(valid, Lk, q.device, fn)
-    n_rows = n_qtok if gathered else Lq
+    n_rows = n_out if gathered else Lq
     if out is None:
-        out = (torch.empty(B, n_qtok, H, D, device=q.device, dtype=torch.bfloat16) if gathered
+        out = (torch.empty(B, n_out, H, D, device=q.device, dtype=torch.bfloat16) if gathered
                else torch.empty_like(q, memory_format=torch.contiguous_format))
+    elif gathered and (out.shape != (B, n_out, H, D) or out.dtype != torch.bfloat16):
+        raise ValueError(f"{fn}: out must be bfloat16 [{B}, {n_out}, {H}, {D}]")
     lse = torch.empty(B, H, n_rows, device=q.device, dtype=torch.float32) if return_lse else None
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q.device, fn)
@@ -577,7 +592,8 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
         indices.stride(0), indices.stride(1), indices.stride(2),
         counts.stride(0), counts.stride(1), counts.stride(2),
         B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes,
-        _ptr(qm), n_qtok, _ptr(km), n_ktok, _stream())
+        _ptr(qm), n_qtok, _ptr(km), n_ktok, _ptr(om), n_out if om is not None else 0,
+        _stream())
     check(st, fn)
     return (out, lse) if return_lse else out
 

@@ -178,3 +178,55 @@ def rcsa_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     out, lse = res if return_lse else (res, None)
     return RCSAResult(out, idx4, cnt3, score, qhat, khat, lse, q_i8, q_scale, k_i8, k_scale,
                       kmean, k_mask)
+
+
+def relay_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layout, selected,
+                    counts, *, int8: bool = True, sm_scale: Optional[float] = None,
+                    return_lse: bool = False, n_split: Optional[int] = None):
+    """The attention core of a causal frame-relay layer: the query-frame rows
+    of a full-world layout attend to every key block the full-layout
+    selection kept (MatrixCausalFrameLayerRelay._current_query_attention,
+    P/matrix_curvature_phase_frame_weave.py:8966-8995, after its selector).
+
+    q, k, v: token-major ``[B, S, H, D]`` over all ``S`` tokens of the frames;
+    ``layout``: a :class:`cast_amd.layout.RelayLayout`; ``selected`` /
+    ``counts``: the selection of every CWCA block ``[B, H, n_blocks, max_k]``
+    / ``[B, H, n_blocks]`` (int32), of which the query blocks' rows are used.
+    Returns the attention output of the query-frame tokens,
+    ``[B, len(layout.query_indices), H, D]`` bf16 in ``query_indices`` order
+    (and the LSE ``[B, H, n]`` with ``return_lse``).  No packed copy is made:
+    the pooling/quantiser passes and the attention read Q, K and V through the
+    layout's slot maps and write the output rows through its query map.
+    D 128 and 128-token blocks.
+    """
+    B, S, H, D = q.shape
+    bs = layout.block_size
+    if D != 128 or bs != 128:
+        raise ValueError("relay_attention: D 128 and 128-token blocks")
+    if k.shape != q.shape or v.shape != q.shape:
+        raise ValueError("relay_attention: q, k and v must be token-major [B, S, H, D] alike")
+    rows = layout.query_block_ids.to(selected.device)
+    idx = selected.index_select(2, rows).to(torch.int32).contiguous()
+    cnt = counts.index_select(2, rows).to(torch.int32).contiguous()
+    n_out = layout.query_indices.numel()
+    scale = 1.0 / math.sqrt(D) if sm_scale is None else sm_scale
+    if int8:
+        # Q quantised over the query rows, K statistics and bits over the key rows
+        _, q_i8, q_scale, _, ksum, kmin, kmax, k_mask = ops.pool_query_key(
+            q, None, k, None, bs, q_slot_token=layout.query_slot_token,
+            k_slot_token=layout.key_slot_token)
+        k_i8, k_scale, _ = ops.quantize_key(k, None, bs, ksum, kmin, kmax,
+                                            slot_token=layout.key_slot_token)
+        v = v if v.dtype == torch.bfloat16 else v.to(torch.bfloat16)
+        return ops.sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, idx, cnt, None,
+                                    block_m=bs, block_n=bs, sm_scale=scale,
+                                    return_lse=return_lse, n_split=n_split,
+                                    block_mask=k_mask, out_token=layout.query_out_row,
+                                    out_len=n_out, v_token=layout.key_slot_token)
+    qb, kb, vb = (x if x.dtype == torch.bfloat16 else x.to(torch.bfloat16) for x in (q, k, v))
+    return ops.sparse_attn_bf16(qb, kb, vb, idx, cnt, None, block_m=bs, block_n=bs,
+                                sm_scale=scale, return_lse=return_lse, n_split=n_split,
+                                block_mask=layout.key_block_mask,
+                                q_token=layout.query_slot_token,
+                                kv_token=layout.key_slot_token,
+                                out_token=layout.query_out_row, out_len=n_out)

@@ -348,8 +348,9 @@ int rcsa_sparse_attn_int8(const int8_t* Q, const float* q_scale,
  * variant also of K — and -1 (or a row >= kv_len) is an empty slot that reads
  * zeros.  The bf16 variant takes q_token (int32 [Q_LEN]) with it: Q row r is
  * token q_token[r] of a token-major Q of q_tokens rows, and O / M are written
- * to that token row ([B, q_tokens, H, D] / [B, H, q_tokens]; -1 rows are
- * dropped), as out_token does for the int8 variant.  Needs K_block_mask,
+ * to row out_token[r] of [B, out_len, H, D] / [B, H, out_len] (-1 rows are
+ * dropped), as out_token does for the int8 variant; with out_token NULL they
+ * go to row q_token[r] of q_tokens rows.  Needs K_block_mask,
  * HEAD_DIM 128, BLOCK_M = BLOCK_N = 128, K_LEN a multiple of 128 and
  * kv_len x (V, bf16 also K) row stride below 2^31 bytes; else RCSA_ERR_SHAPE.
  */
@@ -369,6 +370,7 @@ int rcsa_sparse_attn_bf16_split(const void* Q, const void* K, const void* V,
                                 int64_t max_k, int64_t n_split, void* workspace,
                                 int64_t workspace_bytes, const int32_t* q_token,
                                 int64_t q_tokens, const int32_t* kv_token, int64_t kv_len,
+                                const int32_t* out_token, int64_t out_len,
                                 hipStream_t stream);
 int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
                                 int64_t q_scale_stride, const int8_t* K,

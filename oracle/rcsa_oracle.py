@@ -18,6 +18,9 @@ docstring; the pins live in tests/test_oracle_pins.py:
   sparse_attention    fp64 per-row loops; single-key => v; equal logits => mean(v);
                       per-row shift invariance of softmax
   compact_layout      reference's loop branch restated with pure-Python lists
+  relay_layout        hand-enumerated small grid (block ids from coordinates,
+                      partial-cell query frames); every key token in exactly
+                      one slot, query rows = the key rows' query-frame members
   apportion*          exact rational arithmetic (fractions.Fraction) + conserved sums
   saturate            closed forms: the result sums to min(target, n * cap), never
                       exceeds cap, and only rows below cap before a pass gain
@@ -45,7 +48,7 @@ __all__ = [
     "sparse_attention", "sparse_attention_int8", "equivalence_stats", "compact_layout",
     "apportion", "apportion_section_matrix", "saturate", "budget_blocks", "rcsa_layer",
     "apportion_section_matrix_f32", "compact_time_cells", "redistribute_compact_capacity",
-    "closed_loop_degrees",
+    "closed_loop_degrees", "relay_layout",
 ]
 
 
@@ -365,6 +368,61 @@ def compact_layout(active_frames: Sequence[int], memory_temporal: int, height: i
             idx[b, slot] = tok
             t2p[tok] = b * block_size + slot
     return idx, idx >= 0, t2p
+
+
+def relay_layout(total_temporal: int, memory_temporal: int, height: int, width: int,
+                 block_shape: tuple[int, int, int], query_frames: Sequence[int], *,
+                 protected_current: bool = True):
+    """Asymmetric frame-relay layout: full-world keys, query-frame queries.
+
+    Restates MatrixCausalFrameLayerRelay._asymmetric_layout
+    (P/matrix_curvature_phase_frame_weave.py:8734-8846) with pure-Python
+    lists: a token's block id comes from its (frame, row, column); with a
+    protected current chunk the memory frames and the current frames fill
+    separate temporal cells (:8768-8782).  Key block b holds every token with
+    id b in increasing order (:8795-8801); the query blocks are the sorted
+    ids of the query-frame tokens and hold only those tokens (:8810-8824).
+    Returns dict(key [NB, BS] int64 -1 padded, query_block_ids [NQ] int64,
+    query [NQ, BS] int64 -1 padded, query_indices [n] int64).
+    """
+    tt, th, tw = block_shape
+    spatial = height * width
+    nh, nw = -(-height // th), -(-width // tw)
+    mem = memory_temporal
+    if protected_current:
+        mem_blocks = -(-mem // tt) * nh * nw if mem else 0
+        n_blocks = mem_blocks + -(-(total_temporal - mem) // tt) * nh * nw
+    else:
+        mem_blocks = 0
+        n_blocks = -(-total_temporal // tt) * nh * nw
+    qset = {int(f) for f in query_frames}
+    block_size = tt * th * tw
+    key: list[list[int]] = [[] for _ in range(n_blocks)]
+    qmembers: dict[int, list[int]] = {}
+    query_indices = []
+    for tok in range(total_temporal * spatial):
+        t, r = tok // spatial, tok % spatial
+        h, w = r // width, r % width
+        if protected_current and t >= mem:
+            cell, base = (t - mem) // tt, mem_blocks
+        else:
+            cell, base = t // tt, 0
+        b = base + cell * nh * nw + (h // th) * nw + w // tw
+        key[b].append(tok)
+        if t in qset:
+            qmembers.setdefault(b, []).append(tok)
+            query_indices.append(tok)
+    ids = sorted(qmembers)
+    kidx = torch.full((n_blocks, block_size), -1, dtype=torch.long)
+    for b, mem_ in enumerate(key):
+        if len(mem_) > block_size:
+            raise RuntimeError("CWCA block contains too many tokens")
+        kidx[b, :len(mem_)] = torch.tensor(mem_, dtype=torch.long)
+    qidx = torch.full((len(ids), block_size), -1, dtype=torch.long)
+    for r, b in enumerate(ids):
+        qidx[r, :len(qmembers[b])] = torch.tensor(qmembers[b], dtype=torch.long)
+    return {"key": kidx, "query_block_ids": torch.tensor(ids, dtype=torch.long),
+            "query": qidx, "query_indices": torch.tensor(query_indices, dtype=torch.long)}
 
 
 # --------------------------------------------------------------------------

@@ -380,9 +380,10 @@ def test_sparse_attn_split_lists(dev, int8):
             *cnt_d.stride(), B, H, q.shape[2], k.shape[2], D, bs, bs, idx.shape[3]]
     stream = torch.cuda.current_stream().cuda_stream
     split_args = args[:4] + [None] + args[4:]  # K_block_mask after K_valid
+    no_maps = (None, 0, None, 0, None, 0)  # q_token, kv_token, out_token and their lengths
     assert lib.rcsa_sparse_attn_bf16_split(*split_args, 3, small.data_ptr(), need - 256,
-                                           stream) == 2
-    assert lib.rcsa_sparse_attn_bf16_split(*split_args, 3, None, need, stream) == 1
+                                           *no_maps, stream) == 2
+    assert lib.rcsa_sparse_attn_bf16_split(*split_args, 3, None, need, *no_maps, stream) == 1
     # a K row spanning 16 MiB or more is refused before any launch (the copy
     # addressing multiplies row numbers by the row stride in 24 bits)
     big = list(args)

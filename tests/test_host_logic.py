@@ -27,6 +27,39 @@ def test_compact_layout_matches_oracle(frames, mem_t, H, W, shape):
     assert torch.equal(lay.slot_token[lay.token_to_packed], torch.arange(t2p.numel()))
 
 
+@pytest.mark.parametrize("T,mem,qf,prot", [
+    (3, 1, [2], True), (12, 4, [5, 6, 9], True), (19, 5, list(range(5, 19)), True),
+    (10, 3, [0, 4, 8], False)])
+def test_relay_layout_matches_oracle(T, mem, qf, prot):
+    H, W, shape = (2, 3, (2, 1, 2)) if T == 3 else (22, 40, (4, 4, 8))
+    lay = layout.relay_layout(T, mem, H, W, shape, qf, protected_current=prot,
+                              allow_memory_queries=True)
+    ref = orc.relay_layout(T, mem, H, W, shape, qf, protected_current=prot)
+    bs = lay.block_size
+    assert torch.equal(lay.key_slot_token.long(), ref["key"].reshape(-1))
+    assert torch.equal(lay.query_slot_token.long(), ref["query"].reshape(-1))
+    assert torch.equal(lay.query_block_ids, ref["query_block_ids"])
+    assert torch.equal(lay.query_indices, ref["query_indices"])
+    assert torch.equal(lay.key_valid, ref["key"].reshape(-1) >= 0)
+    # the output row of a query slot is its token's position among the query tokens
+    live = lay.query_slot_token >= 0
+    assert torch.equal(lay.query_indices[lay.query_out_row[live].long()],
+                       lay.query_slot_token[live].long())
+    assert bool((lay.query_out_row[~live] == -1).all())
+    # validity bits: bit i of word w of block n = slot n * bs + 32 w + i
+    if bs % 32 == 0:
+        words = lay.key_block_mask.reshape(-1).long() & 0xFFFFFFFF
+        bits = (words[:, None] >> torch.arange(32)) & 1
+        assert torch.equal(bits.reshape(-1).bool(), lay.key_valid)
+
+
+def test_relay_layout_rejects_memory_queries():
+    with pytest.raises(RuntimeError, match="may not write Memory"):
+        layout.relay_layout(12, 4, 22, 40, (4, 4, 8), [2, 5])
+    with pytest.raises(ValueError):
+        layout.relay_layout(12, 4, 22, 40, (4, 4, 8), [12])
+
+
 def test_compact_layout_rejects_bad_input():
     with pytest.raises(ValueError):
         layout.compact_layout([], 0, 4, 4, (1, 2, 2))

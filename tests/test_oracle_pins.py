@@ -456,6 +456,44 @@ def test_compact_layout_vs_argsort(frames, mem_t, H, W, shape):
     assert int(valid.sum()) == len(bid) and valid.shape == (nb, bs)
 
 
+def test_relay_layout_hand_example():
+    """3 frames (1 memory) of 2 x 3 tokens in (2, 1, 2) blocks, enumerated by hand."""
+    pc = orc.relay_layout(3, 1, 2, 3, (2, 1, 2), [2])
+    P = -1
+    assert pc["key"].tolist() == [[0, 1, P, P], [2, P, P, P], [3, 4, P, P], [5, P, P, P],
+                                  [6, 7, 12, 13], [8, 14, P, P], [9, 10, 15, 16], [11, 17, P, P]]
+    # frame 2 shares its cell with frame 1: the query rows keep frame 2's tokens only
+    assert pc["query_block_ids"].tolist() == [4, 5, 6, 7]
+    assert pc["query"].tolist() == [[12, 13, P, P], [14, P, P, P], [15, 16, P, P], [17, P, P, P]]
+    assert pc["query_indices"].tolist() == list(range(12, 18))
+    un = orc.relay_layout(3, 1, 2, 3, (2, 1, 2), [0, 2], protected_current=False)
+    assert un["key"].tolist() == [[0, 1, 6, 7], [2, 8, P, P], [3, 4, 9, 10], [5, 11, P, P],
+                                  [12, 13, P, P], [14, P, P, P], [15, 16, P, P], [17, P, P, P]]
+    assert un["query_block_ids"].tolist() == list(range(8))
+    assert un["query"][0].tolist() == [0, 1, P, P] and un["query"][4].tolist() == [12, 13, P, P]
+
+
+@pytest.mark.parametrize("T,mem,qf,prot", [(12, 4, [5, 6, 9], True), (19, 5, list(range(5, 19)), True),
+                                           (8, 0, [1, 2, 7], True), (10, 3, [0, 4, 8], False)])
+def test_relay_layout_invariants(T, mem, qf, prot):
+    H, W, shape = 22, 40, (4, 4, 8)
+    r = orc.relay_layout(T, mem, H, W, shape, qf, protected_current=prot)
+    key, q = r["key"], r["query"]
+    flat = key.reshape(-1)
+    members = flat[flat >= 0]
+    assert torch.equal(members.sort().values, torch.arange(T * H * W))  # each token once
+    # rows hold increasing tokens, padding at the end
+    for row in list(key) + list(q):
+        live = row[row >= 0]
+        assert torch.equal(live, live.sort().values) and bool((row[len(live):] < 0).all())
+    # each query row = its key row's members that lie in a query frame
+    qset = set(qf)
+    for b, row in zip(r["query_block_ids"].tolist(), q):
+        want = [t for t in key[b].tolist() if t >= 0 and t // (H * W) in qset]
+        assert row[row >= 0].tolist() == want and want
+    assert r["query_indices"].tolist() == [t for t in range(T * H * W) if t // (H * W) in qset]
+
+
 # ---------------------------------------------------------------- budgets
 
 def test_apportion_textbook_and_invariants():

@@ -41,7 +41,7 @@ def _call(lib, name, q8, qs, k8, ks, v, idx, cnt, n_split, extra):
             out.data_ptr(), idx.data_ptr(), cnt.data_ptr(), *q8.stride()[:3],
             *k8.stride()[:3], *v.stride()[:3], *out.stride()[:3], *idx.stride()[:3],
             *cnt.stride(), B, H, Lq, Lk, D, 128, 128, idx.shape[-1], n_split, *extra,
-            None, 0, torch.cuda.current_stream().cuda_stream)
+            None, 0, None, 0, torch.cuda.current_stream().cuda_stream)
     return st, out, lse
 
 
