@@ -715,8 +715,11 @@ sparse_attn_kernel(AttnArgs a) {
       ks_m[sidx] = fetch_scale(n_m[sidx]);
     }
     if constexpr (GATHER) n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;
-    // gathered: the map reads go out one step ahead of their copies, in
-    // the order every ring iteration keeps (map j+1, copies j, map j+2, ...)
+    // gathered: the map reads of the two prologue steps, then their copies,
+    // then the map read of step 2.  The first ring wait counts the copies of
+    // one step plus one step's map reads as the younger operations, so the
+    // map read of step 2 must come after the copies of step 0: the scheduling
+    // fence keeps the compiler from hoisting it (loads issue in order).
     load_tokens(n_m[0], tk_m[0]);
     load_tokens(n_m[1], tk_m[1]);
 #pragma unroll
@@ -724,7 +727,14 @@ sparse_attn_kernel(AttnArgs a) {
       char* const dst = sidx == 0 ? s_0 : sidx == 1 ? s_1 : s_2;
       if constexpr (kValidCopy) stage_valid_flat(n_m[sidx], dst);
       stage_flat(n_m[sidx], dst, tk_m[sidx]);
-      if (sidx == 0) load_tokens(n_pre, tk_m[2]);
+      // the copies of step 0 stay older than those of step 1 (the first
+      // ring wait leaves one step's copies in flight)
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if constexpr (GATHER) {
+      __builtin_amdgcn_sched_barrier(0);
+      load_tokens(n_pre, tk_m[2]);
+      __builtin_amdgcn_sched_barrier(0);
     }
     if (use_bits) mk_m[0] = mask_words(n_m[0]);
     if constexpr (!GATHER) n_pre = STAGES - 1 < steps ? block_of(STAGES - 1) : -1;

@@ -192,3 +192,39 @@ def test_gathered_inputs_rejected_without_both_maps():
         ops.quantize_key(k, None, 128, *(torch.zeros(2, 90, 128, device=k.device)
                                          for _ in range(3)),
                          slot_token=lay_k.slot_token[:-1])
+
+
+@pytest.mark.parametrize("int8", [False, True])
+def test_gathered_call_repeats_bit_exact_at_layer_size(int8):
+    """24 heads, 4 query frames against 40 memory + 4 current frames (30 x 330
+    blocks, 105 per row): twenty gathered calls in a row each equal pack ->
+    packed call -> unpack.  Guards the ring's first wait, which leaves exactly
+    one step's copies (and map reads) in flight and so depends on the
+    prologue's issue order."""
+    from cast_amd import layout, ops
+    from cast_amd.pipeline import rcsa_attention
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(11)
+    H, D = 24, 128
+    lay_q = layout.compact_layout(range(4), 0, *HW, SHAPE, dev)
+    lay_k = layout.compact_layout(range(44), 40, *HW, SHAPE, dev)
+    q, k, v = (torch.randn(1, n * 880, H, D, device=dev, generator=g).div_(D ** 0.5)
+               .to(torch.bfloat16) for n in (4, 44, 44))
+    nq, nk = lay_q.n_blocks, lay_k.n_blocks
+    forced = torch.zeros(nq, nk, dtype=torch.bool, device=dev)
+    forced[:, nk - 30:] = True
+    k_sel = round(0.25 * (nk - 30)) + 30
+    kw = dict(block_size=128, k_select=k_sel, forced=forced, int8=int8, max_k=k_sel)
+    ref = rcsa_attention(ops.pack_tokens(q, lay_q.slot_token), ops.pack_tokens(k, lay_k.slot_token),
+                         ops.pack_tokens(v, lay_k.slot_token), lay_q.slot_valid, lay_k.slot_valid,
+                         **kw)
+    want = ops.unpack_tokens(ref.out, lay_q.token_to_packed)
+    print(f"gathered layer call x20, int8 {int8}", flush=True)
+    bad = []
+    for it in range(20):
+        got = rcsa_attention(q, k, v, None, None, q_slot_token=lay_q.slot_token32,
+                             k_slot_token=lay_k.slot_token32, **kw).out
+        torch.cuda.synchronize()
+        if not torch.equal(got, want):
+            bad.append(it)
+    assert not bad, f"calls {bad} differ"
