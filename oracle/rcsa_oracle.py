@@ -33,6 +33,15 @@ docstring; the pins live in tests/test_oracle_pins.py:
                       whole layer blocks * mean); uniform curvature gives
                       uniform degrees; a pure-Python Fraction re-derivation
                       on small cases
+  omission_proxy      fp64 loops over rows, candidates and sketch groups
+  route_objective_terms / route_objective_value
+                      the quadratic terms reproduce the brute-force change of
+                      the objective value for every single-row change (with the
+                      identity operator and with random operators)
+  fc_pasm_refine      the identity (with the reference's fallback reasons) for
+                      every missing-transport / disabled case; the chosen swap
+                      equals a brute-force search over every admissible
+                      single swap of the objective value
 """
 from __future__ import annotations
 
@@ -48,7 +57,8 @@ __all__ = [
     "sparse_attention", "sparse_attention_int8", "equivalence_stats", "compact_layout",
     "apportion", "apportion_section_matrix", "saturate", "budget_blocks", "rcsa_layer",
     "apportion_section_matrix_f32", "compact_time_cells", "redistribute_compact_capacity",
-    "closed_loop_degrees", "relay_layout",
+    "closed_loop_degrees", "relay_layout", "omission_proxy", "route_objective_terms",
+    "route_objective_value", "fc_pasm_refine",
 ]
 
 
@@ -635,3 +645,307 @@ def rcsa_layer(q, k, v, q_valid, k_valid, *, block_size: int, k_select, forced=N
                                     block_n=block_size, heads=heads, qblocks=qblocks)
     res.update(out=out, lse=lse)
     return res
+
+
+# --------------------------------------------------------------------------
+# a7: FC-PASM swap router
+
+def omission_proxy(probability: torch.Tensor, pooled_value: torch.Tensor,
+                   candidates: torch.Tensor, *, sketch_groups: int,
+                   eps: float = 1e-6) -> torch.Tensor:
+    """Single-block omission proxy of candidate key blocks, sketched over
+    ``sketch_groups`` equal groups of the value channels.
+
+    Restates estimate_block_omission_error (P/fc_pasm_swap_routing.py:64-106):
+    with o = P v (the pooled attention output of the row) and p_c the
+    candidate's probability, proxy[l] = p_c / (1 - p_c + eps) * (o - v_c),
+    averaged within each channel group.  probability [B, H, Q, K],
+    pooled_value [B, H, K, D], candidates [B, H, Q, L] -> [B, H, Q, L, G].
+    """
+    if probability.ndim != 4 or pooled_value.ndim != 4 or candidates.ndim != 4:
+        raise ValueError("omission proxy expects BHQK, BHKD and BHQL tensors")
+    D = pooled_value.shape[-1]
+    if D % sketch_groups:
+        raise ValueError("value width must be divisible by sketch groups")
+    v = pooled_value.float()
+    out = torch.matmul(probability.float(), v)                        # [B, H, Q, D]
+    B, H, Q, L = candidates.shape
+    cand_v = torch.gather(v[:, :, None].expand(B, H, Q, -1, D), 3,
+                          candidates[..., None].expand(B, H, Q, L, D))
+    p_c = torch.gather(probability.float(), -1, candidates)
+    weight = p_c / (1.0 - p_c + eps)
+    diff = weight[..., None] * (out[..., None, :] - cand_v)
+    return diff.reshape(B, H, Q, L, sketch_groups, D // sketch_groups).mean(-1)
+
+
+def _route_cells(exact_frames, temporal_group_size, temporal_cells):
+    return {int(f): min(int(f) // int(temporal_group_size), temporal_cells - 1)
+            for f in exact_frames}
+
+
+def _route_pairs(exact_frames, current_boundary):
+    """(left, right, skipped targets) of consecutive anchors on one side of the boundary."""
+    out = []
+    for left, right in zip(exact_frames, exact_frames[1:]):
+        if (left < current_boundary) != (right < current_boundary):
+            continue
+        out.append((int(left), int(right), tuple(range(left + 1, right))))
+    return out
+
+
+def _route_operator(operator, pair, exponent, spatial, device):
+    """The FC transport operator of ``pair`` at ``exponent`` ([S, S], output x
+    input), or the identity when there is none (the g = 0 case of
+    P/fc_pasm_swap_routing.py:136-141)."""
+    m = operator(pair, exponent) if operator is not None else None
+    if m is None:
+        return torch.eye(spatial, device=device, dtype=torch.float32), False
+    return m.to(device=device, dtype=torch.float32), True
+
+
+def route_objective_value(error: torch.Tensor, *, temporal_cells: int, spatial: int,
+                          exact_frames, temporal_group_size: int, current_boundary: int,
+                          operator=None, lambda_anchor: float = 1.0,
+                          lambda_reconstruction: float = 1.0) -> torch.Tensor:
+    """Anchor + reconstruction omission objective of the current rows.
+
+    Restates _objective_value (P/fc_pasm_swap_routing.py:550-614): the squared
+    error of every anchor frame's cell, plus, for every frame skipped between
+    two anchors on one side of the current boundary, the squared error
+    propagated to it: (1 - a) T^a e_left + a T^-(1-a) e_right, a the frame's
+    position between the anchors.  error [B, H, cells * S, G]."""
+    view = error.reshape(*error.shape[:2], temporal_cells, spatial, error.shape[-1])
+    cell = _route_cells(exact_frames, temporal_group_size, temporal_cells)
+    count = error.new_zeros(temporal_cells)
+    for f in exact_frames:
+        count[cell[int(f)]] += 1.0
+    value = lambda_anchor * (view.square() * count[None, None, :, None, None]).sum()
+    for left, right, skipped in _route_pairs(exact_frames, current_boundary):
+        el, er = view[:, :, cell[left]], view[:, :, cell[right]]
+        for target in skipped:
+            a = float(target - left) / float(right - left)
+            lm, _ = _route_operator(operator, (left, right), a, spatial, error.device)
+            rm, _ = _route_operator(operator, (left, right), -(1.0 - a), spatial, error.device)
+            prop = (1.0 - a) * torch.einsum("st,bhtg->bhsg", lm, el) + \
+                a * torch.einsum("st,bhtg->bhsg", rm, er)
+            value = value + lambda_reconstruction * prop.square().sum()
+    return value
+
+
+def route_objective_terms(error: torch.Tensor, *, temporal_cells: int, spatial: int,
+                          exact_frames, temporal_group_size: int, current_boundary: int,
+                          operator=None, lambda_anchor: float = 1.0,
+                          lambda_reconstruction: float = 1.0):
+    """Per-row quadratic coefficients of the objective: changing row r's error
+    by d changes the objective by sum_g a_r (2 e_rg d_g + d_g^2) + 2 b_rg d_g.
+
+    Restates _objective_terms (P/fc_pasm_swap_routing.py:414-547): a_r = the
+    anchor count of the row's cell times lambda_anchor plus the diagonal of
+    each reconstruction Hessian; b_r = the Hessians' off-diagonal couplings
+    applied to the current errors (within the cell, and across the two
+    anchor cells).  Returns (a [1, 1, rows, 1], b [B, H, rows, G], used)."""
+    B, H, rows, G = error.shape
+    if rows != temporal_cells * spatial:
+        raise RuntimeError("routing error rows do not match Current cells")
+    view = error.reshape(B, H, temporal_cells, spatial, G)
+    cell = _route_cells(exact_frames, temporal_group_size, temporal_cells)
+    count = error.new_zeros(temporal_cells)
+    for f in exact_frames:
+        count[cell[int(f)]] += 1.0
+    coef = count[:, None].expand(-1, spatial).clone() * lambda_anchor
+    lin = torch.zeros_like(view)
+    used = False
+    for left, right, skipped in _route_pairs(exact_frames, current_boundary):
+        lc, rc = cell[left], cell[right]
+        el, er = view[:, :, lc], view[:, :, rc]
+        for target in skipped:
+            a = float(target - left) / float(right - left)
+            lm, f1 = _route_operator(operator, (left, right), a, spatial, error.device)
+            rm, f2 = _route_operator(operator, (left, right), -(1.0 - a), spatial, error.device)
+            used = used or f1 or f2
+            lo, ro = (1.0 - a) * lm, a * rm
+            if lc == rc:
+                comb = lo + ro
+                hess = lambda_reconstruction * (comb.T @ comb)
+                dg = torch.diagonal(hess)
+                coef[lc] += dg
+                lin[:, :, lc] += torch.einsum("st,bhtg->bhsg", hess, el) - dg[None, None, :, None] * el
+            else:
+                hl = lambda_reconstruction * (lo.T @ lo)
+                hr = lambda_reconstruction * (ro.T @ ro)
+                hx = lambda_reconstruction * (lo.T @ ro)
+                dl, dr = torch.diagonal(hl), torch.diagonal(hr)
+                coef[lc] += dl
+                coef[rc] += dr
+                lin[:, :, lc] += (torch.einsum("st,bhtg->bhsg", hl, el)
+                                  - dl[None, None, :, None] * el
+                                  + torch.einsum("st,bhtg->bhsg", hx, er))
+                lin[:, :, rc] += (torch.einsum("st,bhtg->bhsg", hr, er)
+                                  - dr[None, None, :, None] * er
+                                  + torch.einsum("st,bhtg->bhsg", hx.T, el))
+    return coef.reshape(1, 1, rows, 1), lin.reshape(B, H, rows, G), used
+
+
+def _route_fallback(layer_index, reason, **extra):
+    rec = {"layer_index": int(layer_index), "status": "independent_topk_fallback",
+           "fallback_reason": reason, "swap_count": 0, "fixed_budget": True}
+    rec.update(extra)
+    return rec
+
+
+def _route_affinity(entry) -> float:
+    if not isinstance(entry, dict):
+        return 0.0
+    a = entry.get("mean_affinity", 0.0)
+    return float(a.detach().float().item()) if isinstance(a, torch.Tensor) else float(a)
+
+
+def fc_pasm_refine(score: torch.Tensor, pooled_value: torch.Tensor, selected: torch.Tensor,
+                   counts: torch.Tensor, local: torch.Tensor, *, memory_blocks: int,
+                   spatial_shape, exact_current_frames, temporal_group_size: int,
+                   current_boundary: int, transport, layer_index: int, config,
+                   operator=None):
+    """Fixed-budget coordinate-swap refinement of a top-k route.
+
+    Restates FCPASMLocalCoordinateSwapRouter.refine (P/fc_pasm_swap_routing.py:
+    616-1077) for the historical_only = False configurations: the fallbacks
+    that return the route unchanged (:647-748, 783-819), the 2k candidates of
+    the ranking score + 1e6 local (stable descending order: ties to the lower
+    index), the omission proxy of each candidate, and up to num_swap_rounds
+    rounds that each apply the single best (remove, add) exchange over all
+    current rows when it lowers the objective by more than swap_eps
+    (:843-977), with the same-bank rule when configured.  ``config`` carries the
+    FCPASMSwapRoutingConfig fields; ``operator(pair, exponent)`` gives the FC
+    transport operator of a pair (None: identity).  Returns (selected, record).
+    """
+    cfg = config
+    score = score.detach().float()
+    pooled_value = pooled_value.detach()
+    baseline = selected.clone()
+    sel = selected.clone().long()
+    if cfg.active_layers and layer_index not in cfg.active_layers:
+        return baseline, _route_fallback(layer_index, "layer_not_enabled")
+    N = score.shape[-1]
+    rows_cur = score.shape[-2] - int(memory_blocks)
+    S = int(spatial_shape[0] * spatial_shape[1])
+    if rows_cur <= 0 or rows_cur % S:
+        return baseline, _route_fallback(layer_index, "no_rectangular_current_rows",
+                                         fc_cache_used=False)
+    cells = rows_cur // S
+    frames = tuple(int(f) for f in exact_current_frames)
+    if tuple(sorted(set(frames))) != frames:
+        raise ValueError("routing Exact Current frames must be unique and chronological")
+    pairs = [(l, r) for l, r in zip(frames, frames[1:])
+             if r - l > 1 and (l < current_boundary) == (r < current_boundary)]
+    if cfg.num_swap_rounds == 0 or len(frames) < 2 or not pairs:
+        reason = ("zero_swap_rounds" if cfg.num_swap_rounds == 0 else
+                  "fewer_than_two_exact_anchors" if len(frames) < 2 else "no_skipped_frames")
+        return baseline, _route_fallback(layer_index, reason, fc_cache_used=False)
+    tpairs = transport.get("pairs", {}) if isinstance(transport, dict) else {}
+    matching = [tpairs[p] for p in pairs
+                if isinstance(tpairs.get(p), dict) and isinstance(tpairs[p].get("theta"), torch.Tensor)]
+    affinity = max((_route_affinity(e) for e in matching), default=0.0)
+    strong = bool(matching) and affinity >= cfg.min_transport_affinity
+    if cfg.require_fc_transport and not strong:
+        return baseline, _route_fallback(
+            layer_index, "weak_previous_layer_fc_transport" if matching
+            else "missing_previous_layer_fc_transport",
+            matching_transport_affinity=affinity, fc_cache_used=False, g0_fallback=True)
+    gate = torch.ones(cells, dtype=torch.bool)
+    if cfg.min_pair_transport_affinity > 0.0:
+        gate.zero_()
+        for l, r in pairs:
+            if _route_affinity(tpairs.get((l, r))) < cfg.min_pair_transport_affinity:
+                continue
+            for t in range(l + 1, r):
+                gate[min(t // temporal_group_size, cells - 1)] = True
+        if not bool(gate.any()):
+            return baseline, _route_fallback(layer_index, "no_strong_transport_pair_cells",
+                                             fc_cache_used=bool(matching))
+    row_gate = gate.repeat_interleave(S)
+    K = sel.shape[-1]
+    slot = torch.arange(K)
+    valid = slot[None, None, None] < counts[..., None]
+    hist = valid & (sel < memory_blocks)
+    hist_counts = hist.sum(-1)
+    swap_counts = valid.sum(-1)
+    if int(swap_counts.max()) == 0:
+        return baseline, _route_fallback(layer_index, "no_swappable_kv_selected")
+    L = min(N, cfg.candidate_multiplier * int(swap_counts.max()))
+    ranking = score + local[None, None].to(score.dtype) * 1e6
+    cand = torch.sort(ranking, dim=-1, descending=True, stable=True).indices[..., :L]
+    prob = torch.softmax(score, dim=-1)
+    proxy = omission_proxy(prob, pooled_value, cand, sketch_groups=cfg.sketch_groups)
+    limit = torch.minimum(swap_counts.long() * cfg.candidate_multiplier,
+                          torch.full_like(swap_counts.long(), N))
+    cand_valid = torch.arange(L)[None, None, None] < limit[..., None]
+
+    def member(cur):
+        v = slot[None, None, None] < counts[..., None]
+        return ((cand[..., None] == cur[..., None, :]) & v[..., None, :]).any(-1)
+
+    retained = member(sel)
+    err = (proxy * (cand_valid & ~retained)[..., None]).sum(-2)
+    cur_err = err[..., memory_blocks:, :]
+    okw = dict(temporal_cells=cells, spatial=S, exact_frames=frames,
+               temporal_group_size=temporal_group_size, current_boundary=current_boundary,
+               operator=operator, lambda_anchor=cfg.lambda_anchor,
+               lambda_reconstruction=cfg.lambda_reconstruction)
+    obj_before = route_objective_value(cur_err, **okw)
+    swaps = 0
+    chosen = []
+    m0 = int(memory_blocks)
+    for _ in range(cfg.num_swap_rounds):
+        a, b, _ = route_objective_terms(cur_err, **okw)
+        retained = member(sel)
+        v = slot[None, None, None] < counts[..., None]
+        sel_local = torch.gather(local[None, None].expand(*sel.shape[:2], -1, -1), -1, sel.clamp_min(0))
+        removable = v & ~sel_local
+        addable = cand_valid & ~retained
+        match = (cand[..., None] == sel[..., None, :]).float()        # [B, H, Q, L, K]
+        rem_proxy = torch.einsum("bhqlg,bhqlk->bhqkg", proxy, match)[..., m0:, :, :]
+        add_proxy = proxy[..., m0:, :, :]
+        delta = rem_proxy[..., :, None, :] - add_proxy[..., None, :, :]   # [B, H, R, K, L, G]
+        imp = (a[..., None, None] * (2.0 * cur_err[..., None, None, :] * delta + delta.square())
+               + 2.0 * b[..., None, None, :] * delta).sum(-1)
+        pair_ok = removable[..., m0:, :, None] & addable[..., m0:, None, :]
+        if cfg.min_pair_transport_affinity > 0.0:
+            pair_ok = pair_ok & row_gate[None, None, :, None, None]
+        if cfg.same_bank_only:
+            pair_ok = pair_ok & ((sel[..., m0:, :, None] < m0) == (cand[..., m0:, None, :] < m0))
+        imp = imp.masked_fill(~pair_ok, float("inf"))
+        best, best_flat = imp.flatten(-2).min(dim=-1)
+        flat_best = best.reshape(-1)
+        strongest = int(torch.argmin(flat_best))
+        if cfg.max_swaps_per_call and swaps >= cfg.max_swaps_per_call:
+            break
+        if not bool(flat_best[strongest] < -cfg.swap_eps):
+            break
+        bb, hh, rr = (int(x) for x in torch.unravel_index(torch.tensor(strongest), best.shape))
+        fl = int(best_flat[bb, hh, rr])
+        rs, al = fl // L, fl % L
+        added = int(cand[bb, hh, m0 + rr, al])
+        removed = int(sel[bb, hh, m0 + rr, rs])
+        sel[bb, hh, m0 + rr, rs] = added
+        cur_err = cur_err.clone()
+        cur_err[bb, hh, rr] += rem_proxy[bb, hh, rr, rs] - add_proxy[bb, hh, rr, al]
+        swaps += 1
+        chosen.append({"b": bb, "h": hh, "row": m0 + rr, "slot": rs, "removed": removed,
+                       "added": added, "improvement": float(-flat_best[strongest])})
+    v = slot[None, None, None] < counts[..., None]
+    final_hist = ((sel < m0) & v).sum(-1)
+    if cfg.same_bank_only and not torch.equal(hist_counts, final_hist):
+        raise RuntimeError("same-bank FC-PASM routing changed Memory KV counts")
+    dup = (sel[..., :, None] == sel[..., None, :]) & v[..., :, None] & v[..., None, :] & \
+        torch.triu(torch.ones(K, K, dtype=torch.bool), diagonal=1)
+    if bool(dup.any()):
+        raise RuntimeError("FC-PASM routing emitted duplicate keys")
+    obj_after = route_objective_value(cur_err, **okw)
+    if bool(obj_after > obj_before + 1e-5 * obj_before.abs().clamp_min(1.0)):
+        raise RuntimeError("FC-PASM swap increased its refinement objective")
+    rec = {"layer_index": int(layer_index), "status": "refined", "candidate_max": L,
+           "swap_count": swaps, "objective_before": float(obj_before),
+           "objective_after": float(obj_after), "swaps": chosen, "fixed_budget": True,
+           "historical_budget_before": int(hist_counts.sum()),
+           "historical_budget_after": int(final_hist.sum())}
+    return sel.to(selected.dtype), rec

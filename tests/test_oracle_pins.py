@@ -670,3 +670,180 @@ def test_closed_loop_uniform_and_slips():
     fb = orc.closed_loop_degrees(curv, frames, response=resp, response_weight=1.0, **kw)
     cur, base_cur = fb[18:].reshape(3, 6), good[18:].reshape(3, 6)
     assert torch.all(cur[1] >= base_cur[1]) and int(cur[1].sum()) > int(base_cur[1].sum())
+
+
+# ---------------------------------------------------------------- a7 router
+
+def _route_cfg(**kw):
+    from types import SimpleNamespace
+    base = dict(candidate_multiplier=2, num_swap_rounds=1, swap_eps=1e-6, lambda_anchor=1.0,
+                lambda_reconstruction=1.0, sketch_groups=16, require_fc_transport=False,
+                min_transport_affinity=0.0, min_pair_transport_affinity=0.0,
+                max_swaps_per_call=0, active_layers=(), historical_only=False,
+                same_bank_only=False)
+    base.update(kw)
+    return SimpleNamespace(**base)
+
+
+def _route_case(seed, *, H=2, mem=6, hw=(2, 3), cells=2, D=32, K=7):
+    g = torch.Generator().manual_seed(seed)
+    S = hw[0] * hw[1]
+    N = mem + cells * S
+    qh = torch.nn.functional.normalize(torch.randn(1, H, N, D, generator=g), dim=-1)
+    kh = torch.nn.functional.normalize(torch.randn(1, H, N, D, generator=g), dim=-1)
+    score = qh @ kh.transpose(-1, -2) * 4.0
+    pooled_v = torch.randn(1, H, N, D, generator=g)
+    local = torch.eye(N, dtype=torch.bool)  # the block itself is its only protected edge
+    # selection: the block itself, then the best others by score
+    rank = score + local[None, None] * 1e6
+    sel = torch.sort(rank, dim=-1, descending=True, stable=True).indices[..., :K]
+    counts = torch.randint(3, K + 1, (1, H, N), generator=g)
+    return score, pooled_v, sel, counts, local
+
+
+def test_route_fallbacks_are_identity():
+    """Without transport (or with it switched off) the route comes back unchanged,
+    with the reference's fallback reason (P/fc_pasm_swap_routing.py:647-748)."""
+    score, pv, sel, cnt, local = _route_case(0)
+    kw = dict(memory_blocks=6, spatial_shape=(2, 3), exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, layer_index=22)
+    cast_cfg = _route_cfg(require_fc_transport=True, min_transport_affinity=0.5,
+                          max_swaps_per_call=1, active_layers=(22, 26), same_bank_only=True,
+                          swap_eps=0.1)
+    cases = [
+        (cast_cfg, None, kw, "missing_previous_layer_fc_transport"),
+        (cast_cfg, {"pairs": {(0, 6): {"theta": torch.zeros(1, 1, 1), "mean_affinity": 0.2}}},
+         kw, "weak_previous_layer_fc_transport"),
+        (cast_cfg, None, dict(kw, layer_index=5), "layer_not_enabled"),
+        (_route_cfg(), None, dict(kw, exact_current_frames=(3,)), "fewer_than_two_exact_anchors"),
+        (_route_cfg(), None, dict(kw, exact_current_frames=(3, 4)), "no_skipped_frames"),
+        (_route_cfg(num_swap_rounds=0), None, kw, "zero_swap_rounds"),
+        (_route_cfg(), None, dict(kw, memory_blocks=5), "no_rectangular_current_rows"),
+    ]
+    for cfg, transport, kwargs, reason in cases:
+        out, rec = orc.fc_pasm_refine(score, pv, sel, cnt, local, transport=transport,
+                                      config=cfg, **kwargs)
+        assert torch.equal(out, sel) and rec["fallback_reason"] == reason, reason
+        assert rec["swap_count"] == 0 and rec["status"] == "independent_topk_fallback"
+
+
+def test_omission_proxy_fp64_loops():
+    g = torch.Generator().manual_seed(3)
+    B, H, Q, K, D, L, G = 1, 2, 5, 9, 32, 4, 16
+    prob = torch.softmax(torch.randn(B, H, Q, K, generator=g) * 3, dim=-1)
+    v = torch.randn(B, H, K, D, generator=g)
+    cand = torch.stack([torch.randperm(K, generator=g)[:L] for _ in range(B * H * Q)]).reshape(B, H, Q, L)
+    got = orc.omission_proxy(prob, v, cand, sketch_groups=G)
+    P, V = prob.double(), v.double()
+    for b in range(B):
+        for h in range(H):
+            for q in range(Q):
+                o = [sum(float(P[b, h, q, k]) * float(V[b, h, k, d]) for k in range(K)) for d in range(D)]
+                for li in range(L):
+                    c = int(cand[b, h, q, li])
+                    p = float(P[b, h, q, c])
+                    w = p / (1.0 - p + 1e-6)
+                    for gi in range(G):
+                        ds = range(gi * (D // G), (gi + 1) * (D // G))
+                        want = sum(w * (o[d] - float(V[b, h, c, d])) for d in ds) / len(ds)
+                        assert abs(float(got[b, h, q, li, gi]) - want) < 1e-5
+
+
+def _route_operator_random(seed, S):
+    g = torch.Generator().manual_seed(seed)
+    mats = {}
+
+    def op(pair, exponent):
+        if pair not in mats:
+            mats[pair] = torch.randn(S, S, generator=g) * 0.2
+        return torch.eye(S) + exponent * mats[pair]
+    return op
+
+
+@pytest.mark.parametrize("operator_seed", [None, 5])
+@pytest.mark.parametrize("frames,boundary", [((0, 6), 8), ((0, 3, 7), 8), ((1, 3, 5, 7), 4)])
+def test_route_objective_terms_match_value_changes(operator_seed, frames, boundary):
+    """Changing one row's error by d changes the objective value by exactly the
+    quadratic form the terms predict."""
+    g = torch.Generator().manual_seed(11)
+    S, cells, G = 6, 2, 4
+    op = _route_operator_random(operator_seed, S) if operator_seed is not None else None
+    kw = dict(temporal_cells=cells, spatial=S, exact_frames=frames, temporal_group_size=4,
+              current_boundary=boundary, operator=op, lambda_anchor=0.7,
+              lambda_reconstruction=1.3)
+    e = torch.randn(1, 2, cells * S, G, generator=g).double().float()
+    a, b, used = orc.route_objective_terms(e, **kw)
+    assert used == (operator_seed is not None and any(r - l > 1 for l, r in zip(frames, frames[1:])
+                                                      if (l < boundary) == (r < boundary)))
+    base = orc.route_objective_value(e, **kw)
+    for h in range(2):
+        for r in range(cells * S):
+            d = torch.randn(G, generator=g)
+            e2 = e.clone()
+            e2[0, h, r] += d
+            want = float(orc.route_objective_value(e2, **kw) - base)
+            pred = float((a[0, 0, r, 0] * (2 * e[0, h, r] * d + d * d) + 2 * b[0, h, r] * d).sum())
+            assert abs(pred - want) <= 1e-3 * max(1.0, abs(want)), (h, r, pred, want)
+
+
+@pytest.mark.parametrize("same_bank", [False, True])
+@pytest.mark.parametrize("operator_seed", [None, 7])
+def test_route_swap_is_the_best_single_swap(same_bank, operator_seed):
+    """The refine's swap equals a brute-force search of every admissible
+    (row, removed slot, added candidate) exchange by objective value."""
+    score, pv, sel, cnt, local = _route_case(4)
+    mem, S, cells = 6, 6, 2
+    op = _route_operator_random(operator_seed, S) if operator_seed is not None else None
+    cfg = _route_cfg(same_bank_only=same_bank, max_swaps_per_call=1)
+    kw = dict(memory_blocks=mem, spatial_shape=(2, 3), exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, layer_index=0, transport=None)
+    out, rec = orc.fc_pasm_refine(score, pv, sel, cnt, local, config=cfg, operator=op, **kw)
+    assert rec["status"] == "refined"
+    # brute force, from the oracle's own proxy and candidates
+    N = score.shape[-1]
+    K = sel.shape[-1]
+    L = min(N, 2 * int(cnt.max()))
+    cand = torch.sort(score + local[None, None] * 1e6, dim=-1, descending=True, stable=True).indices[..., :L]
+    proxy = orc.omission_proxy(torch.softmax(score, -1), pv, cand, sketch_groups=16)
+    limit = torch.clamp(cnt * 2, max=N)
+    okw = dict(temporal_cells=cells, spatial=S, exact_frames=(0, 6), temporal_group_size=4,
+               current_boundary=8, operator=op)
+    err = torch.zeros(1, 2, N, proxy.shape[-1])
+    for h in range(2):
+        for r in range(N):
+            kept = set(sel[0, h, r, :cnt[0, h, r]].tolist())
+            for li in range(int(limit[0, h, r])):
+                if int(cand[0, h, r, li]) not in kept:
+                    err[0, h, r] += proxy[0, h, r, li]
+    cur = err[:, :, mem:]
+    base = float(orc.route_objective_value(cur, **okw))
+    best = (0.0, None)
+    for h in range(2):
+        for rr in range(cells * S):
+            r = mem + rr
+            n = int(cnt[0, h, r])
+            kept = sel[0, h, r, :n].tolist()
+            for s_ in range(n):
+                rem = kept[s_]
+                if bool(local[r, rem]):
+                    continue
+                rp = sum((proxy[0, h, r, li] for li in range(L) if int(cand[0, h, r, li]) == rem),
+                         torch.zeros(proxy.shape[-1]))
+                for li in range(int(limit[0, h, r])):
+                    add = int(cand[0, h, r, li])
+                    if add in kept or (same_bank and ((rem < mem) != (add < mem))):
+                        continue
+                    e2 = cur.clone()
+                    e2[0, h, rr] += rp - proxy[0, h, r, li]
+                    imp = float(orc.route_objective_value(e2, **okw)) - base
+                    if imp < best[0] - 1e-9:
+                        best = (imp, (h, r, s_, add))
+    if best[1] is None or best[0] >= -cfg.swap_eps:
+        assert rec["swap_count"] == 0
+    else:
+        h, r, s_, add = best[1]
+        sw = rec["swaps"][0]
+        assert (sw["h"], sw["row"], sw["slot"], sw["added"]) == (h, r, s_, add)
+        assert abs(-sw["improvement"] - best[0]) <= 1e-3 * max(1.0, abs(best[0]))
+        assert int(out[0, h, r, s_]) == add
+        assert rec["objective_after"] <= rec["objective_before"]
