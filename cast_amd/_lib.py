@@ -49,6 +49,10 @@ SIGNATURES: dict[str, list] = {
     "rcsa_attn_noalloc_scratch_bytes": [],
     "rcsa_attn_workspace_bytes": [_I, _I, _I, _I, _I],
     "rcsa_attn_split_plan": [_I, _I, _I, _I, _I, ctypes.POINTER(c_int64)],
+    "rcsa_route_proxy": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, c_float, _P, _P,
+                         _P, _P],
+    "rcsa_route_best_swap": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
+                             c_int, _P, _P, _P],
     "rcsa_pack_tokens": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],
     "rcsa_unpack_tokens": [_P, _I, _I, _I, _I, _P, _I, _P, _P],
     "rcsa_status_string": [c_int],

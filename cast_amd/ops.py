@@ -718,3 +718,68 @@ def unpack_tokens(packed: torch.Tensor, token_slot: torch.Tensor) -> torch.Tenso
     check(_lib.load().rcsa_unpack_tokens(packed.data_ptr(), B, H, n_slots, D, ts.data_ptr(),
                                          L, out.data_ptr(), _stream()), fn)
     return out
+
+
+def route_proxy(score: torch.Tensor, pooled_value: torch.Tensor, local: torch.Tensor,
+                selected: torch.Tensor, counts: torch.Tensor, *, memory_blocks: int,
+                n_cand: int, cand_mult: int, sketch_groups: int, eps: float = 1e-6):
+    """Candidates, omission proxies and errors of the current rows (``rcsa_route_proxy``).
+
+    score [B, H, N, N] fp32, pooled_value [B, H, N, D] fp32, local [N, N] bool,
+    selected [B, H, N, K] and counts [B, H, N] (any integer dtype).  Returns
+    (cand int32 [B*H, R, n_cand], proxy fp32 [B*H, R, n_cand, G], error fp32
+    [B*H, R, G]) with R = N - memory_blocks (P/fc_pasm_swap_routing.py:64-106, 826-868).
+    """
+    fn = "route_proxy"
+    _require_cuda(fn, score, pooled_value, selected, counts)
+    B, H, N, N2 = score.shape
+    if N2 != N or pooled_value.shape[:3] != (B, H, N) or selected.shape[:3] != (B, H, N) \
+            or counts.shape != (B, H, N) or tuple(local.shape) != (N, N):
+        raise ValueError(f"{fn}: score [B, H, N, N], values [B, H, N, D], selected "
+                         "[B, H, N, K], counts [B, H, N] and local [N, N] must agree")
+    D, K, G = pooled_value.shape[3], selected.shape[3], int(sketch_groups)
+    R = N - int(memory_blocks)
+    dev = score.device
+    sc = score.float().contiguous()
+    pv = pooled_value.float().contiguous()
+    lo = _bytes_mask(local, dev)
+    sel = selected.to(torch.int32).contiguous()
+    cnt = counts.to(torch.int32).contiguous()
+    cand = torch.empty(B * H, max(R, 0), n_cand, device=dev, dtype=torch.int32)
+    proxy = torch.empty(B * H, max(R, 0), n_cand, G, device=dev, dtype=torch.float32)
+    error = torch.empty(B * H, max(R, 0), G, device=dev, dtype=torch.float32)
+    check(_lib.load().rcsa_route_proxy(
+        sc.data_ptr(), pv.data_ptr(), lo.data_ptr(), sel.data_ptr(), cnt.data_ptr(), B * H, N,
+        int(memory_blocks), D, K, int(n_cand), int(cand_mult), G, float(eps), cand.data_ptr(),
+        proxy.data_ptr(), error.data_ptr(), _stream()), fn)
+    return cand, proxy, error
+
+
+def route_best_swap(proxy: torch.Tensor, cand: torch.Tensor, local: torch.Tensor,
+                    selected: torch.Tensor, counts: torch.Tensor, coef: torch.Tensor,
+                    linear: torch.Tensor, error: torch.Tensor, *, memory_blocks: int,
+                    cand_mult: int, same_bank: bool, row_gate: Optional[torch.Tensor] = None):
+    """Best single exchange of every current row (``rcsa_route_best_swap``):
+    (best fp32 [B*H, R], flat int32 [B*H, R] = slot * n_cand + candidate, -1 if none)
+    (P/fc_pasm_swap_routing.py:899-950)."""
+    fn = "route_best_swap"
+    _require_cuda(fn, proxy, cand, selected, counts, coef, linear, error)
+    BH, R, L, G = proxy.shape
+    B, H, N, K = selected.shape
+    if B * H != BH or N - int(memory_blocks) != R or cand.shape != (BH, R, L) \
+            or error.shape != (BH, R, G) or linear.reshape(-1).numel() != BH * R * G \
+            or coef.reshape(-1).numel() != R:
+        raise ValueError(f"{fn}: inconsistent proxy/candidate/selection shapes")
+    dev = proxy.device
+    sel = selected.to(torch.int32).contiguous()
+    cnt = counts.to(torch.int32).contiguous()
+    gate = _bytes_mask(row_gate, dev) if row_gate is not None else None
+    best = torch.empty(BH, R, device=dev, dtype=torch.float32)
+    flat = torch.empty(BH, R, device=dev, dtype=torch.int32)
+    check(_lib.load().rcsa_route_best_swap(
+        proxy.contiguous().data_ptr(), cand.contiguous().data_ptr(),
+        _bytes_mask(local, dev).data_ptr(), sel.data_ptr(), cnt.data_ptr(),
+        coef.float().contiguous().data_ptr(), linear.float().contiguous().data_ptr(),
+        error.float().contiguous().data_ptr(), _ptr(gate), B * H, N, int(memory_blocks), K, L,
+        int(cand_mult), G, int(bool(same_bank)), best.data_ptr(), flat.data_ptr(), _stream()), fn)
+    return best, flat

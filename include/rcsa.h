@@ -470,6 +470,47 @@ int rcsa_unpack_tokens(const void* packed, int64_t B, int64_t H, int64_t n_slots
                        int64_t D, const int64_t* token_slot, int64_t L, void* out,
                        hipStream_t stream);
 
+/*
+ * FC-PASM swap router, the per-row device work of
+ * FCPASMLocalCoordinateSwapRouter.refine (P/fc_pasm_swap_routing.py:616-1077).
+ *
+ * rcsa_route_proxy: for every (bh, current row r >= memory_blocks) of the
+ * square block scores score [n_bh][n_blocks][n_blocks] (fp32):
+ *   p = softmax(score row) (fp32, max-subtracted), o = p @ pooled_value
+ *   (pooled_value fp32 [n_bh][n_blocks][head_dim], the masked block means of V);
+ *   cand[bh][r - M][0..n_cand) = the first n_cand blocks by the ranking
+ *   score + 1e6 * local (descending, equal rankings by lower block index);
+ *   proxy[bh][r - M][l][g] = p_c / (1 - p_c + eps) * mean over channel group g of
+ *   (o - pooled_value[c]) for c = cand[l] (estimate_block_omission_error, :64-106);
+ *   error[bh][r - M][g] = sum of proxy[l][g] over l < min(cand_mult * count, n_blocks)
+ *   whose block the row does not keep (its first count entries of selected).
+ * local: uint8 [n_blocks][n_blocks]; selected int32 [n_bh][n_blocks][max_k]; counts
+ * int32 [n_bh][n_blocks].  n_blocks <= 1024, head_dim in {64, 128}, sketch_groups
+ * <= 16 and divides head_dim.
+ *
+ * rcsa_route_best_swap: for every (bh, current row), the admissible exchange
+ * (a kept slot s whose block is not a local edge, a candidate l < the row's limit
+ * that the row does not keep; with same_bank, both in memory or both current;
+ * none when row_gate[r - M] == 0) minimising
+ *   sum_g coef[r - M] (2 e_g d_g + d_g^2) + 2 linear[bh][r - M][g] d_g,
+ *   d = proxy of the removed block (0 if it is not a candidate) - proxy[l],
+ *   e = error[bh][r - M]  (the best-swap search of :899-977);
+ * best[bh][r - M] = that value (+inf if none), best_flat = s * n_cand + l (-1 if
+ * none; equal values go to the lower flat index).  coef fp32 [rows]; linear and
+ * error fp32 [n_bh][rows][sketch_groups]; row_gate uint8 [rows] or NULL.
+ */
+int rcsa_route_proxy(const float* score, const float* pooled_value, const uint8_t* local,
+                     const int32_t* selected, const int32_t* counts, int64_t n_bh,
+                     int64_t n_blocks, int64_t memory_blocks, int64_t head_dim, int64_t max_k,
+                     int64_t n_cand, int64_t cand_mult, int64_t sketch_groups, float eps,
+                     int32_t* cand, float* proxy, float* error, hipStream_t stream);
+int rcsa_route_best_swap(const float* proxy, const int32_t* cand, const uint8_t* local,
+                         const int32_t* selected, const int32_t* counts, const float* coef,
+                         const float* linear, const float* error, const uint8_t* row_gate,
+                         int64_t n_bh, int64_t n_blocks, int64_t memory_blocks, int64_t max_k,
+                         int64_t n_cand, int64_t cand_mult, int64_t sketch_groups,
+                         int same_bank, float* best, int32_t* best_flat, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif
