@@ -177,6 +177,43 @@ def compact_layout_call(seed: int, iters: int) -> dict:
     return {**res, **sizes}
 
 
+def router_call(seed: int, iters: int) -> dict:
+    """One FC-PASM swap-router refinement on a compact Matrix layer (24 heads,
+    303 blocks = 183 memory + 4 cells of 6 x 5 current blocks, 99 kept blocks
+    per row, D 128, anchors 0 and 6 with five skipped frames, a route from the
+    pooled scores' top-k, g = 0 transport), timed by wall clock around the
+    whole call (it reads back the strongest row once per round)."""
+    import torch
+    from cast_amd import layout
+    from cast_amd.router import FCPASMSwapRouter, FCPASMSwapRoutingConfig
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    H, N, M, D, K = 24, 303, 183, 128, 99
+    qh = torch.nn.functional.normalize(torch.randn(1, H, N, D, device=dev, generator=g), dim=-1)
+    kh = torch.nn.functional.normalize(torch.randn(1, H, N, D, device=dev, generator=g), dim=-1)
+    score = qh @ kh.transpose(-1, -2)
+    pooled_v = torch.randn(1, H, N, D, device=dev, generator=g)
+    local = layout.local_stencil(N, 6, 5, dev)
+    sel = torch.sort(score + local[None, None] * 1e6, dim=-1, descending=True,
+                     stable=True).indices[..., :K].to(torch.int32)
+    counts = torch.full((1, H, N), K, device=dev, dtype=torch.int32)
+    router = FCPASMSwapRouter(FCPASMSwapRoutingConfig(max_swaps_per_call=1, same_bank_only=True))
+    kw = dict(score=score, pooled_value=pooled_v, selected=sel, counts=counts, local=local,
+              memory_blocks=M, spatial_shape=(6, 5), exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, transport=None, layer_index=22)
+    _, rec = router.refine(**kw)
+    for _ in range(3):
+        router.refine(**kw)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        router.refine(**kw)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / iters
+    return {"ms_per_refine": ms, "swap_count": rec["swap_count"],
+            "candidates": rec["candidate_max"], "blocks": N, "heads": H}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -187,7 +224,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=24)
     ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer", "compact",
-                                       "compact_bf16"],
+                                       "compact_bf16", "router"],
                     default=None,
                     help="profiling mode: run only this kernel (or the whole int8 layer "
                          "call, or the gathered call on the Matrix latent grid) --steps "
@@ -212,6 +249,10 @@ def main() -> int:
         ms = _events_time(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"only": "copy", "bytes_read": src.numel() * 4,
                           "bytes_written": dst.numel() * 4, "avg_ms": ms}))
+        return 0
+
+    if args.only == "router":
+        print(json.dumps({"only": "router", **router_call(args.seed, args.steps)}))
         return 0
 
     if args.only in ("compact", "compact_bf16"):
@@ -439,6 +480,7 @@ def main() -> int:
         frames_d = torch.arange(3, 19, device=dev, dtype=torch.int32)
         extras["row_budgets_us"]["closed_loop_303"] = 1e3 * _events_time(
             lambda: ops.closed_loop_degrees(curv, frames_d, **cl_kw), iters)
+        extras["fc_pasm_router"] = router_call(args.seed, iters)
 
     line["extras"] = extras
     if not args.no_cpu_baseline:

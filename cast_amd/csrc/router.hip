@@ -17,6 +17,7 @@ constexpr int kRouteThreads = 256;
 constexpr int kRouteMaxBlocks = 1024;
 constexpr int kRouteMaxGroups = 16;
 constexpr int kRouteMaxD = 128;
+constexpr int kRouteMaxDynFloats = 12288;  // 48 KiB of dynamic LDS per workgroup
 
 // Ascending keys order rankings descending, equal rankings by index ascending.
 __device__ __forceinline__ uint64_t rank_key(float r, int i) {
@@ -59,10 +60,11 @@ __global__ void __launch_bounds__(kRouteThreads)
 route_proxy_kernel(RouteArgs a) {
   __shared__ float s_p[kRouteMaxBlocks];
   __shared__ uint64_t s_key[kRouteMaxBlocks];
-  __shared__ float s_part[kRouteThreads];
+  __shared__ float s_part[kRouteThreads * 4];
   __shared__ float s_o[kRouteMaxD];
   __shared__ uint8_t s_kept[kRouteMaxBlocks];
   __shared__ float s_red[4];
+  extern __shared__ float s_px[];  // the row's proxies, n_cand x groups
   const int N = a.n_blocks, rows = N - a.memory_blocks;
   const int64_t bh = blockIdx.x / rows;
   const int row = a.memory_blocks + static_cast<int>(blockIdx.x % rows);
@@ -103,16 +105,38 @@ route_proxy_kernel(RouteArgs a) {
   for (int k = t; k < N; k += kRouteThreads) s_p[k] *= inv;
   __syncthreads();
 
-  // o = P v: D channels, kRouteThreads / D partial sums over the blocks
+  // o = P v: D / 4 float4 columns, kRouteThreads * 4 / D partial sums over the
+  // blocks, four loads in flight per thread
   const int D = a.D;
-  const int parts = kRouteThreads / D;
+  const int c4 = D / 4, parts = kRouteThreads / c4;
   const float* v = a.value + bh * static_cast<int64_t>(N) * D;
   {
-    const int d = t % D, part = t / D;
-    float acc = 0.0f;
-    if (part < parts)
-      for (int k = part; k < N; k += parts) acc = fmaf(s_p[k], v[static_cast<int64_t>(k) * D + d], acc);
-    s_part[t] = acc;
+    const int col = t % c4, part = t / c4;
+    const float4* v4 = reinterpret_cast<const float4*>(v) + col;
+    float4 acc = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    int k = part;
+    for (; k + 3 * parts < N; k += 4 * parts) {
+      float4 w[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) w[u] = v4[static_cast<int64_t>(k + u * parts) * c4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const float p = s_p[k + u * parts];
+        acc.x = fmaf(p, w[u].x, acc.x);
+        acc.y = fmaf(p, w[u].y, acc.y);
+        acc.z = fmaf(p, w[u].z, acc.z);
+        acc.w = fmaf(p, w[u].w, acc.w);
+      }
+    }
+    for (; k < N; k += parts) {
+      const float4 w = v4[static_cast<int64_t>(k) * c4];
+      const float p = s_p[k];
+      acc.x = fmaf(p, w.x, acc.x);
+      acc.y = fmaf(p, w.y, acc.y);
+      acc.z = fmaf(p, w.z, acc.z);
+      acc.w = fmaf(p, w.w, acc.w);
+    }
+    reinterpret_cast<float4*>(s_part)[part * c4 + col] = acc;
   }
   // (the sort's first barrier also publishes s_part)
   for (int kk = 2; kk <= np; kk <<= 1) {
@@ -151,21 +175,32 @@ route_proxy_kernel(RouteArgs a) {
     const float w = p / (1.0f - p + a.eps);
     const float* vc = v + static_cast<int64_t>(c) * D + g * gw;
     float acc = 0.0f;
-    for (int d = 0; d < gw; ++d) acc += w * (s_o[g * gw + d] - vc[d]);
+    if (gw == 8) {  // 16 groups of 128 channels: two 16-byte loads
+      const float4 lo = reinterpret_cast<const float4*>(vc)[0];
+      const float4 hi = reinterpret_cast<const float4*>(vc)[1];
+      const float vv[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+      for (int d = 0; d < 8; ++d) acc += w * (s_o[g * 8 + d] - vv[d]);
+    } else {
+      for (int d = 0; d < gw; ++d) acc += w * (s_o[g * gw + d] - vc[d]);
+    }
     return acc / static_cast<float>(gw);
   };
   for (int e = t; e < L * G; e += kRouteThreads) {
     const int l = e / G, g = e % G;
-    proxy[e] = proxy_of(l, g);
+    const float px = proxy_of(l, g);
+    proxy[e] = px;
+    s_px[e] = px;
     if (g == 0) cand[l] = static_cast<int>(static_cast<uint32_t>(s_key[l]));
   }
+  __syncthreads();
   // the row's error: the proxies of the candidates within its limit that it
-  // does not keep, summed in candidate order (recomputed: the same values)
+  // does not keep, summed in candidate order
   if (t < G) {
     float err = 0.0f;
     for (int l = 0; l < limit && l < L; ++l) {
       const int c = static_cast<int>(static_cast<uint32_t>(s_key[l]));
-      if (!s_kept[c]) err += proxy_of(l, t);
+      if (!s_kept[c]) err += s_px[l * G + t];
     }
     a.error[out_row * G + t] = err;
   }
@@ -188,8 +223,9 @@ struct SwapArgs {
 
 __global__ void __launch_bounds__(kRouteThreads)
 route_swap_kernel(SwapArgs a) {
-  __shared__ float s_rem[kRouteMaxBlocks * kRouteMaxGroups];  // removable slots' proxies
+  extern __shared__ float s_rem[];                                // removable slots' proxies
   __shared__ int s_slot[kRouteMaxBlocks];                         // their slot numbers
+  __shared__ uint8_t s_rmem[kRouteMaxBlocks];                     // removed block in memory
   __shared__ int s_pos[kRouteMaxBlocks];                          // candidate position of a block
   __shared__ uint8_t s_kept[kRouteMaxBlocks];
   __shared__ int s_nrem;
@@ -218,14 +254,15 @@ route_swap_kernel(SwapArgs a) {
     if (b >= 0 && b < N) s_kept[b] = 1;
   }
   __syncthreads();
-  // removable slots (kept, not a protected local edge), in slot order
-  if (t == 0) {
-    int n = 0;
-    for (int s = 0; s < cnt; ++s) {
-      const int32_t b = sel[s];
-      if (b >= 0 && b < N && !loc[b]) s_slot[n++] = s;
+  // removable slots (kept, not a protected local edge), in any order: equal
+  // values are resolved by the flat index, not by this order
+  for (int s = t; s < cnt; s += kRouteThreads) {
+    const int32_t b = sel[s];
+    if (b >= 0 && b < N && !loc[b]) {
+      const int n = atomicAdd(&s_nrem, 1);
+      s_rmem[n] = b < M;
+      s_slot[n] = s;
     }
-    s_nrem = n;
   }
   __syncthreads();
   const int nrem = s_nrem;
@@ -238,9 +275,10 @@ route_swap_kernel(SwapArgs a) {
   __syncthreads();
   const float ca = a.coef[rr];
   float err[kRouteMaxGroups], lin[kRouteMaxGroups];
-  for (int g = 0; g < G; ++g) {
-    err[g] = a.error[out_row * G + g];
-    lin[g] = a.linear[out_row * G + g];
+#pragma unroll
+  for (int g = 0; g < kRouteMaxGroups; ++g) {
+    err[g] = g < G ? a.error[out_row * G + g] : 0.0f;
+    lin[g] = g < G ? a.linear[out_row * G + g] : 0.0f;
   }
   const int limit = min(a.cand_mult * cnt, N);
   float bv = INFINITY;
@@ -250,17 +288,22 @@ route_swap_kernel(SwapArgs a) {
       const int c = cand[l];
       if (l >= limit || s_kept[c]) continue;  // not addable
       float add[kRouteMaxGroups];
-      for (int g = 0; g < G; ++g) add[g] = proxy[static_cast<int64_t>(l) * G + g];
-      const bool add_mem = c < M;
+#pragma unroll
+      for (int g = 0; g < kRouteMaxGroups; ++g)
+        add[g] = g < G ? proxy[static_cast<int64_t>(l) * G + g] : 0.0f;
+      const uint8_t add_mem = c < M;
+      // every lane reads the same removable slot at a time (LDS broadcasts)
       for (int i = 0; i < nrem; ++i) {
-        const int s = s_slot[i];
-        if (a.same_bank && ((sel[s] < M) != add_mem)) continue;
+        if (a.same_bank && s_rmem[i] != add_mem) continue;
         float imp = 0.0f;
-        for (int g = 0; g < G; ++g) {
-          const float dl = s_rem[i * G + g] - add[g];
-          imp += ca * (2.0f * err[g] * dl + dl * dl) + 2.0f * lin[g] * dl;
+#pragma unroll
+        for (int g = 0; g < kRouteMaxGroups; ++g) {
+          if (g < G) {
+            const float dl = s_rem[i * G + g] - add[g];
+            imp += ca * (2.0f * err[g] * dl + dl * dl) + 2.0f * lin[g] * dl;
+          }
         }
-        const int flat = s * L + l;
+        const int flat = s_slot[i] * L + l;
         if (imp < bv || (imp == bv && flat < bf)) {
           bv = imp;
           bf = flat;
@@ -319,13 +362,16 @@ extern "C" int rcsa_route_proxy(const float* score, const float* pooled_value, c
   int st = route_shapes(n_bh, n_blocks, memory_blocks, max_k, n_cand, sketch_groups, cand_mult);
   if (st) return st;
   if (!(head_dim == 64 || head_dim == 128) || head_dim % sketch_groups) return RCSA_ERR_SHAPE;
+  if (n_cand * sketch_groups > kRouteMaxDynFloats) return RCSA_ERR_SHAPE;
+  if (reinterpret_cast<uintptr_t>(pooled_value) & 15u) return RCSA_ERR_ALIGN;
   if (!(eps >= 0.0f)) return RCSA_ERR_SHAPE;
   RouteArgs a{score, pooled_value, local, selected, counts, static_cast<int>(n_blocks),
               static_cast<int>(memory_blocks), static_cast<int>(head_dim),
               static_cast<int>(max_k), static_cast<int>(n_cand), static_cast<int>(cand_mult),
               static_cast<int>(sketch_groups), eps, cand, proxy, error};
   const int64_t grid = n_bh * (n_blocks - memory_blocks);
-  route_proxy_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kRouteThreads), 0, stream>>>(a);
+  const size_t lds = static_cast<size_t>(n_cand * sketch_groups) * sizeof(float);
+  route_proxy_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kRouteThreads), lds, stream>>>(a);
   return launch_status();
 }
 
@@ -342,13 +388,14 @@ extern "C" int rcsa_route_best_swap(const float* proxy, const int32_t* cand, con
   int st = route_shapes(n_bh, n_blocks, memory_blocks, max_k, n_cand, sketch_groups, cand_mult);
   if (st) return st;
   // the removable slots' proxies live in LDS; flat indices stay below 2^31
-  if (max_k * sketch_groups > kRouteMaxBlocks * kRouteMaxGroups) return RCSA_ERR_SHAPE;
+  if (max_k * sketch_groups > kRouteMaxDynFloats) return RCSA_ERR_SHAPE;
   if (max_k * n_cand >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
   SwapArgs a{proxy, cand, local, selected, counts, coef, linear, error, row_gate,
              static_cast<int>(n_blocks), static_cast<int>(memory_blocks),
              static_cast<int>(max_k), static_cast<int>(n_cand), static_cast<int>(cand_mult),
              static_cast<int>(sketch_groups), same_bank ? 1 : 0, best, best_flat};
   const int64_t grid = n_bh * (n_blocks - memory_blocks);
-  route_swap_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kRouteThreads), 0, stream>>>(a);
+  const size_t lds = static_cast<size_t>(max_k * sketch_groups) * sizeof(float);
+  route_swap_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kRouteThreads), lds, stream>>>(a);
   return launch_status();
 }

@@ -92,15 +92,18 @@ class FCPASMSwapRouter:
 
     # ---- the objective over the current cells (torch on the device) ----
     def _matrix(self, transport, pair, shape, exponent, device):
-        spatial = int(shape[0] * shape[1])
-        m = None
+        """The pair's operator at ``exponent``, or None for the identity."""
         if self.operator is not None and isinstance(transport, dict):
             entry = transport.get("pairs", {}).get(pair)
             if isinstance(entry, dict):
                 m = self.operator(transport, pair, shape, exponent)
-        if m is None:
-            return torch.eye(spatial, device=device, dtype=torch.float32), False
-        return m.to(device=device, dtype=torch.float32), True
+                if m is not None:
+                    return m.to(device=device, dtype=torch.float32)
+        return None
+
+    @staticmethod
+    def _f32(x: float) -> torch.Tensor:
+        return torch.tensor(x, dtype=torch.float32)
 
     @staticmethod
     def _cells(frames, group, cells):
@@ -123,10 +126,11 @@ class FCPASMSwapRouter:
         BH, rows, G = error.shape
         view = error.reshape(BH, cells, spatial, G)
         cell = self._cells(frames, group, cells)
-        count = error.new_zeros(cells)
+        count = [0.0] * cells
         for f in frames:
             count[cell[int(f)]] += 1.0
-        coef = count[:, None].expand(-1, spatial).clone() * cfg.lambda_anchor
+        coef = (torch.tensor(count, dtype=torch.float32, device=error.device)[:, None]
+                .expand(-1, spatial).clone() * cfg.lambda_anchor)
         lin = torch.zeros_like(view)
         used = False
         shape = self._grid(transport, spatial)
@@ -135,11 +139,27 @@ class FCPASMSwapRouter:
             el, er = view[:, lc], view[:, rc]
             for target in range(left + 1, right):
                 a = float(target - left) / float(right - left)
-                lm, f1 = self._matrix(transport, (left, right), shape, a, error.device)
-                rm, f2 = self._matrix(transport, (left, right), shape, -(1.0 - a), error.device)
-                used = used or f1 or f2
-                lo, ro = (1.0 - a) * lm, a * rm
+                lm = self._matrix(transport, (left, right), shape, a, error.device)
+                rm = self._matrix(transport, (left, right), shape, -(1.0 - a), error.device)
                 lam = cfg.lambda_reconstruction
+                if lm is None and rm is None:
+                    # identity operators (g = 0): the same products in fp32 scalars
+                    wl, wr, la = self._f32(1.0 - a), self._f32(a), self._f32(lam)
+                    if lc == rc:
+                        c = wl + wr
+                        coef[lc] += float(la * (c * c))
+                    else:
+                        coef[lc] += float(la * (wl * wl))
+                        coef[rc] += float(la * (wr * wr))
+                        x = float(la * (wl * wr))
+                        lin[:, lc] += x * er
+                        lin[:, rc] += x * el
+                    continue
+                used = True
+                eye = torch.eye(spatial, device=error.device, dtype=torch.float32)
+                lm = eye if lm is None else lm
+                rm = eye if rm is None else rm
+                lo, ro = (1.0 - a) * lm, a * rm
                 if lc == rc:
                     comb = lo + ro
                     hess = lam * (comb.T @ comb)
@@ -163,19 +183,21 @@ class FCPASMSwapRouter:
         BH, rows, G = error.shape
         view = error.reshape(BH, cells, spatial, G)
         cell = self._cells(frames, group, cells)
-        count = error.new_zeros(cells)
+        count = [0.0] * cells
         for f in frames:
             count[cell[int(f)]] += 1.0
-        value = cfg.lambda_anchor * (view.square() * count[None, :, None, None]).sum()
+        cw = torch.tensor(count, dtype=torch.float32, device=error.device)
+        value = cfg.lambda_anchor * (view.square() * cw[None, :, None, None]).sum()
         shape = self._grid(transport, spatial)
         for left, right in self._pairs(frames, boundary):
             el, er = view[:, cell[left]], view[:, cell[right]]
             for target in range(left + 1, right):
                 a = float(target - left) / float(right - left)
-                lm, _ = self._matrix(transport, (left, right), shape, a, error.device)
-                rm, _ = self._matrix(transport, (left, right), shape, -(1.0 - a), error.device)
-                prop = ((1.0 - a) * torch.einsum("st,btg->bsg", lm, el)
-                        + a * torch.einsum("st,btg->bsg", rm, er))
+                lm = self._matrix(transport, (left, right), shape, a, error.device)
+                rm = self._matrix(transport, (left, right), shape, -(1.0 - a), error.device)
+                pl = el if lm is None else torch.einsum("st,btg->bsg", lm, el)
+                pr = er if rm is None else torch.einsum("st,btg->bsg", rm, er)
+                prop = (1.0 - a) * pl + a * pr
                 value = value + cfg.lambda_reconstruction * prop.square().sum()
         return value
 
@@ -301,10 +323,11 @@ class FCPASMSwapRouter:
         if cfg.same_bank_only and not torch.equal(hist_before, hist_after):
             raise RuntimeError("same-bank FC-PASM routing changed Memory KV counts")
         s64 = sel.long()
-        dup = ((s64[..., :, None] == s64[..., None, :]) & valid_final[..., :, None]
-               & valid_final[..., None, :]
-               & torch.triu(torch.ones(K, K, dtype=torch.bool, device=dev), diagonal=1))
-        if bool(dup.any()):
+        # duplicates among a row's kept entries: equal neighbours once sorted
+        # (padding slots become distinct values past every block)
+        pad = N + torch.arange(K, device=dev)
+        srt = torch.where(valid_final, s64, pad).sort(dim=-1).values
+        if bool((srt[..., 1:] == srt[..., :-1]).any()):
             raise RuntimeError("FC-PASM routing emitted duplicate keys")
         loc = local.to(device=dev, dtype=torch.bool)
         final_local = torch.gather(loc[None, None].expand(B, H, -1, -1), -1,

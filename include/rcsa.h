@@ -486,7 +486,9 @@ int rcsa_unpack_tokens(const void* packed, int64_t B, int64_t H, int64_t n_slots
  *   whose block the row does not keep (its first count entries of selected).
  * local: uint8 [n_blocks][n_blocks]; selected int32 [n_bh][n_blocks][max_k]; counts
  * int32 [n_bh][n_blocks].  n_blocks <= 1024, head_dim in {64, 128}, sketch_groups
- * <= 16 and divides head_dim.
+ * <= 16 and divides head_dim, n_cand * sketch_groups <= 12288 (and, for
+ * rcsa_route_best_swap, max_k * sketch_groups <= 12288); pooled_value 16-byte
+ * aligned.
  *
  * rcsa_route_best_swap: for every (bh, current row), the admissible exchange
  * (a kept slot s whose block is not a local edge, a candidate l < the row's limit

@@ -137,3 +137,57 @@ def test_selector_argument_checks():
         sel.select(q, q, **{**kw, "block_shape": (2, 4, 8)})
     with pytest.raises(RuntimeError, match="too small"):
         sel.compile_budgets(token_h=22, token_w=40, row_degrees=torch.full((60,), 3))
+
+
+def test_router_config_checks():
+    """The reference's configuration errors (P/fc_pasm_swap_routing.py:39-61)."""
+    from cast_amd.router import FCPASMSwapRoutingConfig as C
+    bad = [dict(candidate_multiplier=0), dict(num_swap_rounds=3), dict(swap_eps=-1.0),
+           dict(swap_eps=float("inf")), dict(lambda_anchor=-1.0),
+           dict(lambda_anchor=0.0, lambda_reconstruction=0.0), dict(sketch_groups=3),
+           dict(min_transport_affinity=1.5), dict(min_pair_transport_affinity=-0.1),
+           dict(max_swaps_per_call=-1), dict(active_layers=(-1,)),
+           dict(historical_only=True, same_bank_only=True)]
+    for kw in bad:
+        with pytest.raises(ValueError):
+            C(**kw)
+    C(candidate_multiplier=2, num_swap_rounds=1, swap_eps=0.10, require_fc_transport=True,
+      min_transport_affinity=0.5, max_swaps_per_call=1, active_layers=(22, 26),
+      same_bank_only=True)
+
+
+def test_router_fallbacks_on_the_host():
+    """Every identity case is decided before any device work, with the
+    reference's fallback reasons, and matches the oracle's restatement."""
+    from cast_amd.router import FCPASMSwapRouter, FCPASMSwapRoutingConfig as C
+    g = torch.Generator().manual_seed(0)
+    N, K = 18, 5
+    score = torch.randn(1, 2, N, N, generator=g)
+    pv = torch.randn(1, 2, N, 32, generator=g)
+    sel = torch.sort(score, dim=-1, descending=True).indices[..., :K]
+    cnt = torch.full((1, 2, N), K)
+    local = torch.eye(N, dtype=torch.bool)
+    kw = dict(memory_blocks=6, spatial_shape=(2, 3), exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, layer_index=22)
+    cast = C(require_fc_transport=True, min_transport_affinity=0.5, max_swaps_per_call=1,
+             active_layers=(22, 26), same_bank_only=True, swap_eps=0.1)
+    weak = {"pairs": {(0, 6): {"theta": torch.zeros(1, 1, 1), "mean_affinity": torch.tensor(0.2)}}}
+    cases = [(cast, None, kw), (cast, weak, kw), (cast, None, dict(kw, layer_index=3)),
+             (C(), None, dict(kw, exact_current_frames=(2,))),
+             (C(), None, dict(kw, exact_current_frames=(2, 3))),
+             (C(num_swap_rounds=0), None, kw), (C(), None, dict(kw, memory_blocks=5)),
+             (C(min_pair_transport_affinity=0.9), weak, kw)]
+    router = FCPASMSwapRouter(cast)
+    for cfg, transport, k in cases:
+        router.config = cfg
+        out, rec = router.refine(score=score, pooled_value=pv, selected=sel, counts=cnt,
+                                 local=local, transport=transport, **k)
+        _, want = orc.fc_pasm_refine(score, pv, sel, cnt, local, transport=transport,
+                                     config=cfg, **k)
+        assert torch.equal(out, sel) and rec["status"] == "independent_topk_fallback"
+        assert rec["fallback_reason"] == want["fallback_reason"], (rec, want)
+    assert len(router.summary()["records"]) == len(cases)
+    with pytest.raises(ValueError, match="chronological"):
+        router.config = C()
+        router.refine(score=score, pooled_value=pv, selected=sel, counts=cnt, local=local,
+                      transport=None, **dict(kw, exact_current_frames=(6, 0)))
