@@ -120,4 +120,4 @@ extern "C" const char* rcsa_status_string(int status) {
   }
 }
 
-extern "C" int rcsa_abi_version(void) { return (2 << 16) | 1; }
+extern "C" int rcsa_abi_version(void) { return 3 << 16; }

@@ -40,7 +40,7 @@ def test_library_exports_every_declared_symbol(lib):
 
 def test_status_strings_and_version(lib):
     # host-only entry points: no device work
-    assert lib.rcsa_abi_version() >> 16 >= 1
+    assert lib.rcsa_abi_version() == 3 << 16  # gathered attention sources, router
     for code in range(8):
         assert lib.rcsa_status_string(code)
     assert b"unknown" in lib.rcsa_status_string(99).lower()
