@@ -16,8 +16,9 @@ quadratic terms (small [S, S] operator products over the current cells), the
 choice of the strongest row and the checks at the end are torch on the same
 device, as in the reference.  The FC transport operator of an anchor pair
 comes from ``operator(transport, pair, spatial_shape, exponent)`` (a [S, S]
-matrix, output x input) when the router is given one; without it, and for
-every pair the transport does not hold, the operator is the identity (the
+matrix, output x input; by default ``cast_amd.transport.fc_transport_operator``,
+built from the transport's published phases); for every pair the transport
+does not hold, or with ``operator=None``, the operator is the identity (the
 reference's g = 0 propagation).  The historical-only ablation is not built.
 """
 from __future__ import annotations
@@ -29,6 +30,7 @@ from typing import Any, Callable, Optional
 import torch
 
 from . import ops
+from .transport import fc_transport_operator
 
 
 @dataclass(frozen=True)
@@ -85,7 +87,8 @@ class FCPASMSwapRouter:
     ``FCPASMLocalCoordinateSwapRouter``), its per-row work on the device."""
 
     def __init__(self, config: FCPASMSwapRoutingConfig,
-                 operator: Optional[Callable[..., Optional[torch.Tensor]]] = None) -> None:
+                 operator: Optional[Callable[..., Optional[torch.Tensor]]] = fc_transport_operator
+                 ) -> None:
         self.config = config
         self.operator = operator
         self._records: list[dict[str, Any]] = []

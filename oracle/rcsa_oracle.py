@@ -38,6 +38,9 @@ docstring; the pins live in tests/test_oracle_pins.py:
                       the quadratic terms reproduce the brute-force change of
                       the objective value for every single-row change (with the
                       identity operator and with random operators)
+  transport_maps      exponent 0 and theta 0 give no change; the windows are cut
+                      and overlap-added with explicit index loops (a different
+                      formulation from the product's unfold/fold)
   fc_pasm_refine      the identity (with the reference's fallback reasons) for
                       every missing-transport / disabled case; the chosen swap
                       equals a brute-force search over every admissible
@@ -58,7 +61,7 @@ __all__ = [
     "apportion", "apportion_section_matrix", "saturate", "budget_blocks", "rcsa_layer",
     "apportion_section_matrix_f32", "compact_time_cells", "redistribute_compact_capacity",
     "closed_loop_degrees", "relay_layout", "omission_proxy", "route_objective_terms",
-    "route_objective_value", "fc_pasm_refine",
+    "route_objective_value", "fc_pasm_refine", "transport_maps",
 ]
 
 
@@ -949,3 +952,56 @@ def fc_pasm_refine(score: torch.Tensor, pooled_value: torch.Tensor, selected: to
            "historical_budget_before": int(hist_counts.sum()),
            "historical_budget_after": int(final_hist.sum())}
     return sel.to(selected.dtype), rec
+
+
+def transport_maps(transport: dict, pair, maps: torch.Tensor, exponent: float) -> torch.Tensor:
+    """Change of ``maps`` [N, C, h, w] (the attention block grid) under an
+    anchor pair's FC transport at ``exponent``.
+
+    Restates _apply_transport_maps (P/fc_pasm_swap_routing.py:271-412) with
+    explicit loops over the overlap windows: bilinear lift to the output grid,
+    reflect padding, square-root Hann windows, 2x average pooling to the
+    transport grid when it is smaller, spectrum times exp(i exponent g theta),
+    back to pixels (and up to the window), weighted overlap-add normalised by
+    the summed squared window, the transported minus the zero-phase result,
+    averaged over ceil-sized blocks back onto the h x w grid."""
+    e = transport["pairs"][pair]
+    theta, gain = e["theta"].float(), e["affinity"].float()
+    oh, ow = transport["output_shape"]
+    th, tw = transport["transport_shape"]
+    wh, ww = transport["window_shape"]
+    sh, sw = transport["stride"]
+    ph, pw = transport["padding"]
+    n, c, h, w = maps.shape
+    wy = torch.hann_window(wh, periodic=False, dtype=torch.float32)
+    wx = torch.hann_window(ww, periodic=False, dtype=torch.float32)
+    win = torch.sqrt(torch.clamp(wy[:, None] * wx[None, :], min=0.0))
+    up = F.interpolate(maps.float(), size=(oh, ow), mode="bilinear", align_corners=False)
+    pad = F.pad(up, (pw, pw, ph, ph), mode="reflect")
+    H2, W2 = oh + 2 * ph, ow + 2 * pw
+    acc_m = torch.zeros(n, c, H2, W2)
+    acc_s = torch.zeros(n, c, H2, W2)
+    norm = torch.zeros(H2, W2)
+    t = 0
+    for y in range(0, H2 - wh + 1, sh):
+        for x in range(0, W2 - ww + 1, sw):
+            tile = pad[:, :, y:y + wh, x:x + ww] * win
+            if (th, tw) != (wh, ww):
+                tile = F.avg_pool2d(tile, 2, 2, ceil_mode=True, count_include_pad=False)
+            spec = torch.fft.rfft2(tile)
+            rot = torch.polar(torch.ones_like(theta[t]), exponent * gain[t] * theta[t])
+            mv = torch.fft.irfft2(spec * rot, s=(th, tw))
+            st = torch.fft.irfft2(spec, s=(th, tw))
+            if (th, tw) != (wh, ww):
+                mv = F.interpolate(mv, size=(wh, ww), mode="bilinear", align_corners=False)
+                st = F.interpolate(st, size=(wh, ww), mode="bilinear", align_corners=False)
+            acc_m[:, :, y:y + wh, x:x + ww] += mv * win
+            acc_s[:, :, y:y + wh, x:x + ww] += st * win
+            norm[y:y + wh, x:x + ww] += win * win
+            t += 1
+    if t != theta.shape[0]:
+        raise RuntimeError("FC transport tiles do not match the overlap grid")
+    nrm = norm[ph:ph + oh, pw:pw + ow].clamp_min(1e-8)
+    diff = (acc_m - acc_s)[:, :, ph:ph + oh, pw:pw + ow] / nrm
+    bh, bw = -(-oh // h), -(-ow // w)
+    return F.avg_pool2d(diff, (bh, bw), (bh, bw), ceil_mode=True, count_include_pad=False)

@@ -128,3 +128,43 @@ def test_cast_configuration_is_identity_without_transport(dev):
     assert len(s["records"]) == 3 and s["config"]["active_layers"] == [22, 26]
     router.reset()
     assert router.summary()["records"] == []
+
+
+def test_refine_with_published_transport(dev):
+    """A strong published transport (per-window phases and affinities, the
+    corrector's window geometry): the router's default operator against the
+    oracle's window-loop transport, two rounds."""
+    import math
+    from cast_amd.router import FCPASMSwapRouter
+    score, pv, sel, cnt, local = _case(9)
+    g = torch.Generator().manual_seed(9)
+    theta = (torch.rand(18, 6, 3, generator=g) * 2 - 1) * math.pi
+    gain = torch.rand(18, 6, 3, generator=g)
+    geo = {"output_shape": (22, 40), "transport_shape": (6, 5), "window_shape": (11, 10),
+           "stride": (8, 8), "padding": (4, 5), "tile_grid": (3, 6),
+           "attention_spatial_h": HW[0], "attention_spatial_w": HW[1]}
+    host_tr = dict(geo, pairs={(0, 6): {"theta": theta, "affinity": gain,
+                                        "mean_affinity": torch.tensor(0.9)}})
+    dev_tr = dict(geo, pairs={(0, 6): {"theta": theta.to(dev), "affinity": gain.to(dev),
+                                       "mean_affinity": torch.tensor(0.9)}})
+    S = HW[0] * HW[1]
+    eye = torch.eye(S).reshape(S, 1, *HW)
+
+    def oracle_op(pair, exponent):
+        d = orc.transport_maps(host_tr, pair, eye, exponent).reshape(S, S)
+        return (torch.eye(S) + d).T
+    cfg = _cfg(num_swap_rounds=2, require_fc_transport=True, min_transport_affinity=0.5)
+    kw = dict(memory_blocks=MEM, spatial_shape=HW, exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, layer_index=22)
+    want, rec_w = orc.fc_pasm_refine(score, pv, sel, cnt, local, transport=host_tr, config=cfg,
+                                     operator=oracle_op, **kw)
+    print("refine with published transport", flush=True)
+    got, rec = FCPASMSwapRouter(cfg).refine(score=score.to(dev), pooled_value=pv.to(dev),
+                                            selected=sel.to(dev), counts=cnt.to(dev),
+                                            local=local.to(dev), transport=dev_tr, **kw)
+    torch.cuda.synchronize()
+    assert rec["status"] == "refined" and rec["fc_cache_used"] and not rec["g0_fallback"]
+    assert rec["swap_count"] == rec_w["swap_count"] >= 1
+    assert torch.equal(got.cpu(), want)
+    assert abs(float(rec["objective_after"]) - rec_w["objective_after"]) <= \
+        1e-4 * abs(rec_w["objective_after"])

@@ -191,3 +191,30 @@ def test_router_fallbacks_on_the_host():
         router.config = C()
         router.refine(score=score, pooled_value=pv, selected=sel, counts=cnt, local=local,
                       transport=None, **dict(kw, exact_current_frames=(6, 0)))
+
+
+def test_transport_operator_matches_oracle():
+    """The router's [S, S] operator (unit maps through unfold/fold) against the
+    oracle's window loops, on random maps; cached per exponent; None without
+    a usable entry."""
+    import math
+    from cast_amd.transport import fc_transport_operator, transport_maps
+    g = torch.Generator().manual_seed(4)
+    theta = (torch.rand(18, 6, 3, generator=g) * 2 - 1) * math.pi
+    tr = {"output_shape": (22, 40), "transport_shape": (6, 5), "window_shape": (11, 10),
+          "stride": (8, 8), "padding": (4, 5), "tile_grid": (3, 6),
+          "pairs": {(0, 6): {"theta": theta, "affinity": torch.rand(18, 6, 3, generator=g),
+                             "mean_affinity": torch.tensor(0.8)}}}
+    maps = torch.randn(4, 1, 6, 5, generator=g)
+    for a in (0.25, -0.6):
+        op = fc_transport_operator(tr, (0, 6), (6, 5), a)
+        want = maps + orc.transport_maps(tr, (0, 6), maps, a)
+        got = (op @ maps.reshape(4, 30).T).T.reshape(4, 1, 6, 5)
+        torch.testing.assert_close(got, want, atol=2e-5, rtol=1e-4)
+        assert fc_transport_operator(tr, (0, 6), (6, 5), a) is op
+    multi = torch.randn(2, 3, 6, 5, generator=g)
+    torch.testing.assert_close(transport_maps(tr, (0, 6), multi, 0.4),
+                               orc.transport_maps(tr, (0, 6), multi, 0.4), atol=2e-5, rtol=1e-4)
+    assert torch.equal(fc_transport_operator(tr, (0, 6), (6, 5), 0.0), torch.eye(30))
+    assert fc_transport_operator(tr, (1, 6), (6, 5), 0.5) is None
+    assert fc_transport_operator(None, (0, 6), (6, 5), 0.5) is None

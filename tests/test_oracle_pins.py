@@ -847,3 +847,28 @@ def test_route_swap_is_the_best_single_swap(same_bank, operator_seed):
         assert abs(-sw["improvement"] - best[0]) <= 1e-3 * max(1.0, abs(best[0]))
         assert int(out[0, h, r, s_]) == add
         assert rec["objective_after"] <= rec["objective_before"]
+
+
+def _transport(seed, zero_theta=False):
+    g = torch.Generator().manual_seed(seed)
+    theta = (torch.rand(18, 6, 3, generator=g) * 2 - 1) * math.pi
+    if zero_theta:
+        theta = torch.zeros_like(theta)
+    return {"output_shape": (22, 40), "transport_shape": (6, 5), "window_shape": (11, 10),
+            "stride": (8, 8), "padding": (4, 5), "tile_grid": (3, 6),
+            "pairs": {(0, 6): {"theta": theta, "affinity": torch.rand(18, 6, 3, generator=g),
+                               "mean_affinity": torch.tensor(0.8)}}}
+
+
+def test_transport_maps_identities():
+    """No phase (exponent 0, or theta 0) moves nothing; a phase moves something."""
+    g = torch.Generator().manual_seed(2)
+    maps = torch.randn(3, 2, 6, 5, generator=g)
+    tr = _transport(1)
+    assert float(orc.transport_maps(tr, (0, 6), maps, 0.0).abs().max()) == 0.0
+    assert float(orc.transport_maps(_transport(1, True), (0, 6), maps, 0.7).abs().max()) == 0.0
+    moved = orc.transport_maps(tr, (0, 6), maps, 0.5)
+    assert moved.shape == maps.shape and float(moved.abs().max()) > 1e-3
+    # linear in the maps
+    both = orc.transport_maps(tr, (0, 6), maps[:1] + 2 * maps[1:2], 0.5)
+    torch.testing.assert_close(both, moved[:1] + 2 * moved[1:2], atol=1e-5, rtol=1e-5)
