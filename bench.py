@@ -214,6 +214,38 @@ def router_call(seed: int, iters: int) -> dict:
             "candidates": rec["candidate_max"], "blocks": N, "heads": H}
 
 
+def qkv_call(seed: int, iters: int) -> dict:
+    """The shared int8 Q/K/V projection of a Matrix self-attention block:
+    38,720 tokens x 3072 channels (44 frames of 22 x 40) into q, k and v of
+    3072 channels each, bf16 in and out, random int8 weights: one per-token
+    quantisation, three int8 GEMMs with the dequantising epilogue."""
+    import torch
+    from types import SimpleNamespace
+    from cast_amd import ops
+    from cast_amd.qkv import shared_int8_qkv
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    L, C = 38720, 3072
+    mods = [SimpleNamespace(in_features=C, out_features=C,
+                            weight_int8=torch.randint(-127, 128, (C, C), device=dev, generator=g,
+                                                      dtype=torch.int8),
+                            weight_scales=torch.rand(C, device=dev, generator=g) * 2e-3,
+                            bias=torch.randn(C, device=dev, generator=g).bfloat16())
+            for _ in range(3)]
+    x = torch.randn(1, L, C, device=dev, generator=g).bfloat16()
+    xq, xs = ops.quantize_rows_int8(x)
+    gemm_ms = _events_time(lambda: ops.int8_linear(xq, xs, mods[0].weight_int8,
+                                                   mods[0].weight_scales, mods[0].bias), iters)
+    quant_ms = _events_time(lambda: ops.quantize_rows_int8(x), iters)
+    call_ms = _events_time(lambda: shared_int8_qkv(*mods, x), iters)
+    ops_gemm = 2.0 * L * C * C
+    return {"ms_per_call": call_ms, "quantize_ms": quant_ms, "gemm_ms": gemm_ms,
+            "gemm_TOPS": ops_gemm / gemm_ms / 1e9,
+            "gemm_frac_int8_peak": ops_gemm / gemm_ms / 1e9 / INT8_PEAK_TOPS,
+            "quantize_GBs": (L * C * 3 + L * 4) / quant_ms / 1e6,
+            "tokens": L, "channels": C}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -224,7 +256,7 @@ def main() -> int:
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=24)
     ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer", "compact",
-                                       "compact_bf16", "router"],
+                                       "compact_bf16", "router", "qkv"],
                     default=None,
                     help="profiling mode: run only this kernel (or the whole int8 layer "
                          "call, or the gathered call on the Matrix latent grid) --steps "
@@ -249,6 +281,10 @@ def main() -> int:
         ms = _events_time(lambda: dst.copy_(src), args.steps, args.warmup)
         print(json.dumps({"only": "copy", "bytes_read": src.numel() * 4,
                           "bytes_written": dst.numel() * 4, "avg_ms": ms}))
+        return 0
+
+    if args.only == "qkv":
+        print(json.dumps({"only": "qkv", **qkv_call(args.seed, args.steps)}))
         return 0
 
     if args.only == "router":
@@ -481,6 +517,7 @@ def main() -> int:
         extras["row_budgets_us"]["closed_loop_303"] = 1e3 * _events_time(
             lambda: ops.closed_loop_degrees(curv, frames_d, **cl_kw), iters)
         extras["fc_pasm_router"] = router_call(args.seed, iters)
+        extras["int8_qkv_projection"] = qkv_call(args.seed, iters)
 
     line["extras"] = extras
     if not args.no_cpu_baseline:

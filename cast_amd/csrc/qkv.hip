@@ -1,0 +1,282 @@
+// Shared int8 Q/K/V projection (gfx950): one per-token int8 quantisation of
+// the activations, then int8 GEMMs with a dequantising epilogue.
+//
+// quant_rows_kernel: one wavefront per token row; scale = absmax / 127 (1 for
+// an all-zero row), q = rne(x * 127 / absmax) clamped to [-127, 127].
+//
+// int8_linear_kernel: out[m][n] = bf16(bf16(acc * xs[m] * ws[n]) + bias[n]),
+// acc = sum_k x[m][k] w[n][k] in int32.  A workgroup (4 wavefronts) computes a
+// 128 (tokens) x 256 (channels) tile; each wavefront 64 x 128 as 2 x 4 tiles of
+// v_mfma_i32_32x32x32_i8 with the weights as the A operand, so a lane ends up
+// holding one token and runs of 4 consecutive channels (8-byte stores).  Both
+// operands are staged by direct-to-LDS copies through a 3-slot ring of 64-byte
+// K steps (24 KiB per slot); 16-byte chunks of each 64-byte row are XORed by
+// (row / 4) mod 4 so the ds_read_b128 operand reads are conflict free.
+#include <type_traits>
+
+#include "rcsa_common.h"
+
+#define RCSA_QKV_LDS(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+namespace rcsa {
+
+constexpr int kQThreads = 256;       // quantiser: 4 rows per workgroup
+constexpr int kGemmThreads = 256;    // 4 wavefronts
+constexpr int kTM = 128, kTN = 256;  // workgroup tile (tokens x channels)
+constexpr int kKS = 64;              // bytes of K per ring step
+constexpr int kXBytes = kTM * kKS;   // 8 KiB
+constexpr int kWBytes = kTN * kKS;   // 16 KiB
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T v) {
+  if constexpr (std::is_same<T, float>::value) return v;
+  else return bf16_to_f32(v);
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kQThreads)
+quant_rows_kernel(const T* x, int64_t M, int64_t C, int64_t ldx, int8_t* q, float* scale) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (kQThreads / kWave) + threadIdx.x / kWave;
+  if (row >= M) return;
+  const T* xr = x + row * ldx;
+  float amax = 0.0f;
+  for (int64_t c = lane * 8; c < C; c += kWave * 8) {
+    float v[8];
+    Vec8<T>::load(xr + c, v);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+  }
+  amax = wave_max(amax);
+  const float inv = amax > 0.0f ? 127.0f / amax : 1.0f;
+  if (lane == 0) scale[row] = amax > 0.0f ? amax / 127.0f : 1.0f;
+  int8_t* qr = q + row * C;
+  for (int64_t c = lane * 8; c < C; c += kWave * 8) {
+    float v[8];
+    Vec8<T>::load(xr + c, v);
+    uint32_t lo = 0, hi = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      lo |= (static_cast<uint32_t>(quant_i8(v[j], inv)) & 0xffu) << (8 * j);
+      hi |= (static_cast<uint32_t>(quant_i8(v[j + 4], inv)) & 0xffu) << (8 * j);
+    }
+    *reinterpret_cast<uint2*>(qr + c) = make_uint2(lo, hi);
+  }
+}
+
+struct LinearArgs {
+  const int8_t* x;      // [M, K]
+  const float* xs;      // [M]
+  const int8_t* w;      // [N, K]
+  const float* ws;      // [N]
+  const u16* bias;      // [N] bf16 or NULL
+  u16* out;             // [M, ldo] bf16
+  int64_t M, N, K, ldo;
+  int64_t tiles_n;      // N / kTN
+};
+
+constexpr int kQkvRsrc3 = 0x00020000;  // raw untyped buffer, 32-bit data format
+
+__device__ __forceinline__ void dma16(const int8_t* base, int bytes, uint32_t voff, int soff,
+                                      char* dst) {
+  const __amdgpu_buffer_rsrc_t r =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<int8_t*>(base), 0, bytes, kQkvRsrc3);
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RCSA_QKV_LDS(void, dst), 16, voff, soff, 0, 0);
+}
+
+// chunk XOR of a 64-byte row: (row / 4) mod 4
+__device__ __forceinline__ int qkv_swz(int row) { return (row >> 2) & 3; }
+
+// s_waitcnt immediate for vmcnt <= n only (gfx9 encoding)
+constexpr int qkv_vmcnt(int n) {
+  return (n & 0xf) | (0x7 << 4) | (0xf << 8) | (((n >> 4) & 0x3) << 14);
+}
+
+template <int N>
+__device__ __forceinline__ void qkv_wait_barrier() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
+}
+
+__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+int8_linear_kernel(LinearArgs a) {
+  __shared__ __attribute__((aligned(1024))) char s_0[kXBytes + kWBytes];
+  __shared__ __attribute__((aligned(1024))) char s_1[kXBytes + kWBytes];
+  __shared__ __attribute__((aligned(1024))) char s_2[kXBytes + kWBytes];
+  // XCD-aware order: consecutive tiles of one XCD share the token rows (the
+  // channel tiles of a row block run back to back on one L2)
+  const int64_t n_tiles = ((a.M + kTM - 1) / kTM) * a.tiles_n;
+  const int64_t tile = xcd_remap(blockIdx.x, n_tiles);
+  if (tile < 0) return;
+  const int64_t tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  const int64_t m0 = tm * kTM, n0 = tn * kTN;
+  const int t = threadIdx.x, lane = t % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // copies: the 8 KiB token tile is 8 units of 1 KiB (16 rows each), the 16 KiB
+  // weight tile 16 units; a wavefront copies 2 + 4 units per ring step.  Lane l
+  // lands at row 16 u + l / 4, chunk l % 4 of its unit and loads the chunk that
+  // the swizzle puts there.
+  const int64_t rows_x = a.M - m0 < kTM ? a.M - m0 : kTM;
+  const int8_t* xb = a.x + m0 * a.K;
+  const int8_t* wb = a.w + n0 * a.K;
+  const int xbytes = static_cast<int>(rows_x * a.K), wbytes = static_cast<int>(kTN * a.K);
+  uint32_t xoff[2], woff[4];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int r = (wave * 2 + i) * 16 + lane / 4;
+    xoff[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = (wave * 4 + i) * 16 + lane / 4;
+    woff[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
+  }
+  auto stage = [&](int s, char* dst) __attribute__((always_inline)) {
+    const int k0 = s * kKS;  // past the last step: re-copy step 0 (never read)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) dma16(xb, xbytes, xoff[i], k0, dst + (wave * 2 + i) * 1024);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      dma16(wb, wbytes, woff[i], k0, dst + kXBytes + (wave * 4 + i) * 1024);
+  };
+  constexpr int kOps = 6;
+
+  // operand read offsets: row r of a tile, chunk c = 2 ks + lane half
+  const int hf = lane >> 5, li = lane & 31;
+  int xo[2][2], wo[4][2];
+#pragma unroll
+  for (int tmi = 0; tmi < 2; ++tmi)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r = wm * 64 + tmi * 32 + li;
+      xo[tmi][ks] = r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
+    }
+#pragma unroll
+  for (int tni = 0; tni < 4; ++tni)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r = wn * 128 + tni * 32 + li;
+      wo[tni][ks] = kXBytes + r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
+    }
+
+  v16i acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
+
+  const int steps = static_cast<int>(a.K / kKS);
+  stage(0, s_0);
+  stage(steps > 1 ? 1 : 0, s_1);
+  auto compute = [&](const char* tile, int s_fill, char* fill) __attribute__((always_inline)) {
+    v4i xf[2][2], wf[4][2];
+#pragma unroll
+    for (int tmi = 0; tmi < 2; ++tmi)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) xf[tmi][ks] = *reinterpret_cast<const v4i*>(tile + xo[tmi][ks]);
+#pragma unroll
+    for (int tni = 0; tni < 4; ++tni)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) wf[tni][ks] = *reinterpret_cast<const v4i*>(tile + wo[tni][ks]);
+    stage(s_fill, fill);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int tni = 0; tni < 4; ++tni)
+#pragma unroll
+        for (int tmi = 0; tmi < 2; ++tmi)
+          acc[tni][tmi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[tni][ks], xf[tmi][ks],
+                                                                acc[tni][tmi], 0, 0, 0);
+  };
+  // ring: step j lives in slot j % 3; the copies of step j + 2 go out while
+  // step j is computed (steps past the end re-copy step 0 so every
+  // wavefront always has kOps copies per step in flight)
+  // (the host keeps the step count a multiple of 3)
+  for (int j = 0; j < steps; j += 3) {
+    qkv_wait_barrier<kOps>();
+    compute(s_0, j + 2 < steps ? j + 2 : 0, s_2);
+    qkv_wait_barrier<kOps>();
+    compute(s_1, j + 3 < steps ? j + 3 : 0, s_0);
+    qkv_wait_barrier<kOps>();
+    compute(s_2, j + 4 < steps ? j + 4 : 0, s_1);
+  }
+  __builtin_amdgcn_s_waitcnt(qkv_vmcnt(0));
+
+  // epilogue: lane holds token m = li of each 32-token tile and channels
+  // 8 g + 4 hf + (0..3) of each 32-channel tile
+#pragma unroll
+  for (int tmi = 0; tmi < 2; ++tmi) {
+    const int64_t m = m0 + wm * 64 + tmi * 32 + li;
+    if (m >= a.M) continue;
+    const float xs = a.xs[m];
+    u16* orow = a.out + m * a.ldo;
+#pragma unroll
+    for (int tni = 0; tni < 4; ++tni)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int64_t n = n0 + wn * 128 + tni * 32 + 8 * g + 4 * hf;
+        const float4 ws = *reinterpret_cast<const float4*>(a.ws + n);
+        float y[4] = {static_cast<float>(acc[tni][tmi][4 * g + 0]) * xs * ws.x,
+                      static_cast<float>(acc[tni][tmi][4 * g + 1]) * xs * ws.y,
+                      static_cast<float>(acc[tni][tmi][4 * g + 2]) * xs * ws.z,
+                      static_cast<float>(acc[tni][tmi][4 * g + 3]) * xs * ws.w};
+        if (a.bias != nullptr) {
+          const uint2 bb = *reinterpret_cast<const uint2*>(a.bias + n);
+          const float bv[4] = {__uint_as_float(bb.x << 16), __uint_as_float(bb.x & 0xffff0000u),
+                               __uint_as_float(bb.y << 16), __uint_as_float(bb.y & 0xffff0000u)};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) y[e] = bf16_to_f32(f32_to_bf16(y[e])) + bv[e];
+        }
+        *reinterpret_cast<uint2*>(orow + n) =
+            make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+      }
+  }
+}
+
+}  // namespace rcsa
+
+using namespace rcsa;
+
+extern "C" int rcsa_quantize_rows_int8(const void* x, int dtype, int64_t M, int64_t C, int64_t ldx,
+                                       int8_t* q, float* scale, hipStream_t stream) {
+  if (!x || !q || !scale) return RCSA_ERR_NULL;
+  if (M <= 0 || C <= 0 || C % 8 || ldx < C || ldx % 8) return RCSA_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(q) & 7u))
+    return RCSA_ERR_ALIGN;
+  const int64_t rows_per = kQThreads / kWave;
+  const dim3 grid(static_cast<unsigned>((M + rows_per - 1) / rows_per));
+  if (dtype == RCSA_BF16)
+    quant_rows_kernel<u16><<<grid, dim3(kQThreads), 0, stream>>>(static_cast<const u16*>(x), M, C,
+                                                                  ldx, q, scale);
+  else if (dtype == RCSA_F32)
+    quant_rows_kernel<float><<<grid, dim3(kQThreads), 0, stream>>>(static_cast<const float*>(x), M,
+                                                                    C, ldx, q, scale);
+  else
+    return RCSA_ERR_DTYPE;
+  return launch_status();
+}
+
+extern "C" int rcsa_int8_linear(const int8_t* x, const float* x_scale, const int8_t* w,
+                                const float* w_scale, const void* bias, int64_t M, int64_t N,
+                                int64_t K, void* out, int64_t ldo, hipStream_t stream) {
+  if (!x || !x_scale || !w || !w_scale || !out) return RCSA_ERR_NULL;
+  if (M <= 0 || N <= 0 || K <= 0 || N % kTN || K % (3 * kKS) || ldo < N || ldo % 4)
+    return RCSA_ERR_SHAPE;
+  // the copies address a tile with 32-bit offsets
+  if (static_cast<int64_t>(kTN) * K >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
+  if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
+      (reinterpret_cast<uintptr_t>(w_scale) & 15u) || (reinterpret_cast<uintptr_t>(out) & 7u) ||
+      (reinterpret_cast<uintptr_t>(bias) & 7u))
+    return RCSA_ERR_ALIGN;
+  LinearArgs a{x, x_scale, w, w_scale, static_cast<const u16*>(bias), static_cast<u16*>(out),
+               M, N, K, ldo, N / kTN};
+  const int64_t tiles = ((M + kTM - 1) / kTM) * a.tiles_n;
+  if (tiles >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
+  const dim3 grid(static_cast<unsigned>(xcd_grid(tiles)));
+  int8_linear_kernel<<<grid, dim3(kGemmThreads), 0, stream>>>(a);
+  return launch_status();
+}

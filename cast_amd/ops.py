@@ -783,3 +783,53 @@ def route_best_swap(proxy: torch.Tensor, cand: torch.Tensor, local: torch.Tensor
         error.float().contiguous().data_ptr(), _ptr(gate), B * H, N, int(memory_blocks), K, L,
         int(cand_mult), G, int(bool(same_bank)), best.data_ptr(), flat.data_ptr(), _stream()), fn)
     return best, flat
+
+
+def quantize_rows_int8(x: torch.Tensor):
+    """Per-token symmetric int8 quantisation of ``x [..., C]`` (``rcsa_quantize_rows_int8``):
+    (q int8 [M, C], scale fp32 [M]) with M the product of the leading dims."""
+    fn = "quantize_rows_int8"
+    _require_cuda(fn, x)
+    if x.dtype == torch.float16:
+        x = x.float()
+    code = _dtype_code(x, fn)
+    x2 = x.reshape(-1, x.shape[-1])
+    if x2.stride(1) != 1:
+        x2 = x2.contiguous()
+    M, C = x2.shape
+    q = torch.empty(M, C, device=x.device, dtype=torch.int8)
+    scale = torch.empty(M, device=x.device, dtype=torch.float32)
+    check(_lib.load().rcsa_quantize_rows_int8(x2.data_ptr(), code, M, C, x2.stride(0),
+                                              q.data_ptr(), scale.data_ptr(), _stream()), fn)
+    return q, scale
+
+
+def int8_linear(x_i8: torch.Tensor, x_scale: torch.Tensor, w_i8: torch.Tensor,
+                w_scale: torch.Tensor, bias: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16 ``(x_i8 @ w_i8^T) * x_scale[:, None] * w_scale[None, :] (+ bias)`` on int8
+    MFMA (``rcsa_int8_linear``); x_i8 [M, K], w_i8 [N, K] int8."""
+    fn = "int8_linear"
+    _require_cuda(fn, x_i8, x_scale, w_i8, w_scale)
+    if x_i8.dtype != torch.int8 or w_i8.dtype != torch.int8:
+        raise TypeError(f"{fn}: x and w must be int8")
+    x_i8, w_i8 = x_i8.contiguous(), w_i8.contiguous()
+    M, K = x_i8.shape
+    N, K2 = w_i8.shape
+    if K2 != K:
+        raise ValueError(f"{fn}: x [M, {K}] and w [N, {K2}] disagree")
+    xs = x_scale.reshape(-1).float().contiguous()
+    ws = w_scale.reshape(-1).float().contiguous()
+    if xs.numel() != M or ws.numel() != N:
+        raise ValueError(f"{fn}: need {M} token scales and {N} channel scales")
+    b = bias.reshape(-1).to(torch.bfloat16).contiguous() if bias is not None else None
+    if b is not None and b.numel() != N:
+        raise ValueError(f"{fn}: bias must have {N} entries")
+    if out is None:
+        out = torch.empty(M, N, device=x_i8.device, dtype=torch.bfloat16)
+    if out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1:
+        raise ValueError(f"{fn}: out must be bfloat16 [{M}, {N}] with contiguous rows")
+    check(_lib.load().rcsa_int8_linear(x_i8.data_ptr(), xs.data_ptr(), w_i8.data_ptr(),
+                                       ws.data_ptr(), _ptr(b), M, N, K, out.data_ptr(),
+                                       out.stride(0), _stream()), fn)
+    return out

@@ -513,6 +513,30 @@ int rcsa_route_best_swap(const float* proxy, const int32_t* cand, const uint8_t*
                          int64_t n_cand, int64_t cand_mult, int64_t sketch_groups,
                          int same_bank, float* best, int32_t* best_flat, hipStream_t stream);
 
+/*
+ * Shared int8 Q/K/V projection (P/matrix_shared_int8_qkv.py:19-92): the
+ * activations are quantised once per token and reused by the three int8
+ * projections.  No reference kernel: the reference calls the upstream Matrix
+ * Int8Linear Triton kernels (int8_quantize_triton, int8_gemm_triton), which it
+ * does not vendor.
+ *
+ * rcsa_quantize_rows_int8: x [M][C] (row stride ldx; bf16 or fp32, 16-byte
+ * aligned, C and ldx multiples of 8) -> q int8 [M][C] (row stride C, 8-byte
+ * aligned), scale fp32 [M]: scale = absmax_c |x| / 127 (1 for an all-zero row),
+ * q = clamp(rne(x * 127 / absmax), -127, 127).
+ *
+ * rcsa_int8_linear: out[m][n] = bf16(bf16(float(acc) * x_scale[m] * w_scale[n])
+ * + bias[n]), acc = sum_k x[m][k] w[n][k] (int32), for x int8 [M][K], w int8
+ * [N][K] (both 16-byte aligned), w_scale fp32 [N] (16-byte aligned), bias bf16
+ * [N] or NULL (then out = bf16(float(acc) * x_scale * w_scale)); out bf16 with
+ * row stride ldo (8-byte aligned).  N a multiple of 256, K a multiple of 192.
+ */
+int rcsa_quantize_rows_int8(const void* x, int dtype, int64_t M, int64_t C, int64_t ldx,
+                            int8_t* q, float* scale, hipStream_t stream);
+int rcsa_int8_linear(const int8_t* x, const float* x_scale, const int8_t* w, const float* w_scale,
+                     const void* bias, int64_t M, int64_t N, int64_t K, void* out, int64_t ldo,
+                     hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

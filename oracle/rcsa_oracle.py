@@ -41,6 +41,9 @@ docstring; the pins live in tests/test_oracle_pins.py:
   transport_maps      exponent 0 and theta 0 give no change; the windows are cut
                       and overlap-added with explicit index loops (a different
                       formulation from the product's unfold/fold)
+  quantize_rows_int8  error <= scale / 2, the absmax element maps to +-127, zero rows
+  int8_linear         pure-Python integer dot products on small shapes; exact
+                      int32 accumulation bound; scales factor out
   fc_pasm_refine      the identity (with the reference's fallback reasons) for
                       every missing-transport / disabled case; the chosen swap
                       equals a brute-force search over every admissible
@@ -61,7 +64,8 @@ __all__ = [
     "apportion", "apportion_section_matrix", "saturate", "budget_blocks", "rcsa_layer",
     "apportion_section_matrix_f32", "compact_time_cells", "redistribute_compact_capacity",
     "closed_loop_degrees", "relay_layout", "omission_proxy", "route_objective_terms",
-    "route_objective_value", "fc_pasm_refine", "transport_maps",
+    "route_objective_value", "fc_pasm_refine", "transport_maps", "quantize_rows_int8",
+    "int8_linear",
 ]
 
 
@@ -1005,3 +1009,34 @@ def transport_maps(transport: dict, pair, maps: torch.Tensor, exponent: float) -
     diff = (acc_m - acc_s)[:, :, ph:ph + oh, pw:pw + ow] / nrm
     bh, bw = -(-oh // h), -(-ow // w)
     return F.avg_pool2d(diff, (bh, bw), (bh, bw), ceil_mode=True, count_include_pad=False)
+
+
+# --------------------------------------------------------------------------
+# f4: shared int8 Q/K/V projection
+
+def quantize_rows_int8(x: torch.Tensor):
+    """Per-token symmetric int8 quantisation, the shared step of
+    shared_int8_qkv (P/matrix_shared_int8_qkv.py:79-84; the upstream
+    int8_quantize_triton is not vendored, so its arithmetic is restated as
+    stated): scale = absmax / 127 (1 for an all-zero row), q = clamp(rne(x * 127
+    / absmax), -127, 127).  x [..., C] -> (q int8 [M, C], scale fp32 [M])."""
+    x2 = x.reshape(-1, x.shape[-1]).float()
+    amax = x2.abs().amax(dim=1)
+    # (a tensor numerator: python-scalar / tensor would multiply by a rounded reciprocal)
+    inv = torch.where(amax > 0, torch.tensor(127.0) / amax, torch.ones_like(amax))
+    scale = torch.where(amax > 0, amax / 127.0, torch.ones_like(amax))
+    q = torch.clamp(torch.round(x2 * inv[:, None]), -127, 127).to(torch.int8)
+    return q, scale
+
+
+def int8_linear(x_i8: torch.Tensor, x_scale: torch.Tensor, w_i8: torch.Tensor,
+                w_scale: torch.Tensor, bias: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One projection of shared_int8_qkv (P/matrix_shared_int8_qkv.py:19-38):
+    the exact integer product x_i8 @ w_i8^T, dequantised in fp32 as
+    (acc * x_scale[m]) * w_scale[n], rounded to bf16, then + bias in bf16."""
+    acc = x_i8.to(torch.int64) @ w_i8.to(torch.int64).T
+    y = (acc.to(torch.float32) * x_scale.float()[:, None]) * w_scale.float()[None, :]
+    y = y.to(torch.bfloat16)
+    if bias is not None:
+        y = y + bias.to(torch.bfloat16)
+    return y

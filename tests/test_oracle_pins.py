@@ -872,3 +872,38 @@ def test_transport_maps_identities():
     # linear in the maps
     both = orc.transport_maps(tr, (0, 6), maps[:1] + 2 * maps[1:2], 0.5)
     torch.testing.assert_close(both, moved[:1] + 2 * moved[1:2], atol=1e-5, rtol=1e-5)
+
+
+# ---------------------------------------------------------------- f4 int8 QKV
+
+def test_quantize_rows_int8_bounds():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(40, 64, generator=g) * torch.rand(40, 1, generator=g) * 10
+    x[3] = 0.0
+    q, s = orc.quantize_rows_int8(x)
+    assert q.dtype == torch.int8 and int(q.abs().max()) <= 127
+    err = (q.float() * s[:, None] - x).abs()
+    assert bool((err <= s[:, None] / 2 + 1e-6).all())
+    live = torch.arange(40) != 3
+    assert bool((q[live].abs().amax(dim=1) == 127).all())
+    assert float(s[3]) == 1.0 and int(q[3].abs().max()) == 0
+    q2, s2 = orc.quantize_rows_int8(q.float() * s[:, None])   # idempotent on its grid
+    assert torch.equal(q2, q)
+
+
+def test_int8_linear_integer_loops():
+    g = torch.Generator().manual_seed(6)
+    M, N, K = 5, 7, 33
+    x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    xs, ws = torch.rand(M, generator=g) * 0.02, torch.rand(N, generator=g) * 0.02
+    bias = torch.randn(N, generator=g)
+    got = orc.int8_linear(x, xs, w, ws, bias)
+    for m in range(M):
+        for n in range(N):
+            acc = sum(int(x[m, k]) * int(w[n, k]) for k in range(K))
+            y = torch.tensor(acc, dtype=torch.float32) * xs[m] * ws[n]
+            want = y.to(torch.bfloat16) + bias[n].to(torch.bfloat16)
+            assert got[m, n] == want
+    # the largest product a 3072-wide projection can accumulate stays exact in int32
+    assert 3072 * 127 * 127 < 2 ** 31
