@@ -103,12 +103,19 @@ int8_linear_kernel(LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char s_0[kXBytes + kWBytes];
   __shared__ __attribute__((aligned(1024))) char s_1[kXBytes + kWBytes];
   __shared__ __attribute__((aligned(1024))) char s_2[kXBytes + kWBytes];
-  // XCD-aware order: consecutive tiles of one XCD share the token rows (the
-  // channel tiles of a row block run back to back on one L2)
-  const int64_t n_tiles = ((a.M + kTM - 1) / kTM) * a.tiles_n;
+  // XCD-aware order in groups of kGroupM token blocks: consecutive tiles of one
+  // XCD walk the group's token blocks for one channel block, then the next
+  // channel block, so the workgroups resident on an XCD at once share a few
+  // token blocks and a few weight blocks in its L2 (16 blocks: 0.47 ms against
+  // 0.59 ms for whole rows of channel blocks at 38,720 x 3072 x 3072)
+  constexpr int64_t kGroupM = 16;
+  const int64_t n_m = (a.M + kTM - 1) / kTM;
+  const int64_t n_tiles = n_m * a.tiles_n;
   const int64_t tile = xcd_remap(blockIdx.x, n_tiles);
   if (tile < 0) return;
-  const int64_t tm = tile / a.tiles_n, tn = tile % a.tiles_n;
+  const int64_t group = tile / (kGroupM * a.tiles_n), in_group = tile % (kGroupM * a.tiles_n);
+  const int64_t group_m = n_m - group * kGroupM < kGroupM ? n_m - group * kGroupM : kGroupM;
+  const int64_t tm = group * kGroupM + in_group % group_m, tn = in_group / group_m;
   const int64_t m0 = tm * kTM, n0 = tn * kTN;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
