@@ -386,7 +386,7 @@ sparse_attn_kernel(AttnArgs a) {
   auto load_tokens = [&](int n, uint32_t (&tk)[kTokArr]) __attribute__((always_inline)) {
     if constexpr (GATHER) {
       const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<int32_t*>(a.kv_tok), 0, klen * 4, kRsrcWord3);
+          const_cast<int32_t*>(a.kv_tok), 0, n < 0 ? 0 : klen * 4, kRsrcWord3);
       const int key0 = (n < 0 ? 0 : n) * BNS;
 #pragma unroll
       for (int i = 0; i < kTok; ++i)
@@ -397,6 +397,10 @@ sparse_attn_kernel(AttnArgs a) {
   auto row_off = [&](uint32_t t, uint32_t row_bytes, uint32_t col) __attribute__((always_inline)) {
     return t < kv_rows ? t * row_bytes + col : 0x80000000u;
   };
+  // A step past the list (n < 0) still issues its copies, so that every
+  // ring wait counts the same operations, but through empty buffer ranges:
+  // every lane is out of range, nothing is read from memory and the slot,
+  // which nobody reads, fills with zeros.
   auto stage_flat = [&](int n, char* dst, const uint32_t (&tk)[kTokArr]) __attribute__((always_inline)) {
     if constexpr (GATHER) {
       char* const kb0 = const_cast<char*>(kbase);
@@ -404,18 +408,18 @@ sparse_attn_kernel(AttnArgs a) {
       if constexpr (INT8) {  // packed int8 keys: the step's rows as in the flat copy
         int key0 = (n < 0 ? 0 : n) * BNS;
         char* const kbs = kb0 + static_cast<uint64_t>(static_cast<uint32_t>(key0)) * krb;
-        const int knum = BNS * static_cast<int>(krb);
+        const int knum = n < 0 ? 0 : BNS * static_cast<int>(krb);
 #pragma unroll
         for (int i = 0; i < C::KUPW; ++i)
           buffer_copy16(kbs, knum, k_lo[i], dst + (wave * C::KUPW + i) * 1024);
       } else {
-        const int knum = static_cast<int>(kv_rows * krb);
+        const int knum = n < 0 ? 0 : static_cast<int>(kv_rows * krb);
 #pragma unroll
         for (int i = 0; i < C::KUPW; ++i)
           buffer_copy16(kb0, knum, row_off(tk[i], krb, k_lo[i]),
                         dst + (wave * C::KUPW + i) * 1024);
       }
-      const int vnum = static_cast<int>(kv_rows * vrb);
+      const int vnum = n < 0 ? 0 : static_cast<int>(kv_rows * vrb);
 #pragma unroll
       for (int i = 0; i < C::VUPW; ++i)
         buffer_copy16(vb0, vnum, row_off(tk[i], vrb, v_lo[i]),
@@ -425,7 +429,7 @@ sparse_attn_kernel(AttnArgs a) {
     int key0 = (n < 0 ? 0 : n) * BNS;
     key0 = key0 > klast ? klast : key0;
     const int left = klen - key0;  // >= 1
-    const int rows = left < BNS ? left : BNS;
+    const int rows = n < 0 ? 0 : (left < BNS ? left : BNS);
     // (key0 and the row strides are below 2^31: 32 x 32 -> 64-bit products)
     char* const kb0 = const_cast<char*>(kbase) +
                       static_cast<uint64_t>(static_cast<uint32_t>(key0)) * krb;
@@ -450,7 +454,7 @@ sparse_attn_kernel(AttnArgs a) {
     const bool has = a.kvalid != nullptr;
     char* const vb = has ? reinterpret_cast<char*>(const_cast<uint8_t*>(a.kvalid)) + key0
                          : reinterpret_cast<char*>(kAllValid);
-    const int left = has ? klen - key0 : BNS;
+    const int left = n < 0 ? 0 : (has ? klen - key0 : BNS);
     const int vnum = ((left + 3) & ~3) < BNS ? ((left + 3) & ~3) : BNS;
     buffer_copy4(vb, vnum, 4u * (lane & 31), dst + C::BUF);
   };
