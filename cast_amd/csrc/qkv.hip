@@ -5,13 +5,14 @@
 // an all-zero row), q = rne(x * 127 / absmax) clamped to [-127, 127].
 //
 // int8_linear_kernel: out[m][n] = bf16(bf16(acc * xs[m] * ws[n]) + bias[n]),
-// acc = sum_k x[m][k] w[n][k] in int32.  A workgroup (4 wavefronts) computes a
-// 128 (tokens) x 256 (channels) tile; each wavefront 64 x 128 as 2 x 4 tiles of
-// v_mfma_i32_32x32x32_i8 with the weights as the A operand, so a lane ends up
-// holding one token and runs of 4 consecutive channels (8-byte stores).  Both
-// operands are staged by direct-to-LDS copies through a 3-slot ring of 64-byte
-// K steps (24 KiB per slot); 16-byte chunks of each 64-byte row are XORed by
-// (row / 4) mod 4 so the ds_read_b128 operand reads are conflict free.
+// acc = sum_k x[m][k] w[n][k] in int32.  A workgroup (8 wavefronts, one per CU)
+// computes a 256 (tokens) x 256 (channels) tile; each wavefront 64 x 128 as
+// 2 x 4 tiles of v_mfma_i32_32x32x32_i8 with the weights as the A operand, so a
+// lane ends up holding one token and runs of 4 consecutive channels (8-byte
+// stores).  Both operands are staged by direct-to-LDS copies through a 3-slot
+// ring of 64-byte K steps (32 KiB per slot); 16-byte chunks of each 64-byte row
+// are XORed by (row / 4) mod 4 so the ds_read_b128 operand reads are conflict
+// free.
 #include <type_traits>
 
 #include "rcsa_common.h"
@@ -21,10 +22,10 @@
 namespace rcsa {
 
 constexpr int kQThreads = 256;       // quantiser: 4 rows per workgroup
-constexpr int kGemmThreads = 256;    // 4 wavefronts
-constexpr int kTM = 128, kTN = 256;  // workgroup tile (tokens x channels)
+constexpr int kGemmThreads = 512;    // 8 wavefronts: 4 (tokens) x 2 (channels)
+constexpr int kTM = 256, kTN = 256;  // workgroup tile (tokens x channels)
 constexpr int kKS = 64;              // bytes of K per ring step
-constexpr int kXBytes = kTM * kKS;   // 8 KiB
+constexpr int kXBytes = kTM * kKS;   // 16 KiB
 constexpr int kWBytes = kTN * kKS;   // 16 KiB
 
 template <typename T>
@@ -105,10 +106,10 @@ int8_linear_kernel(LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char s_2[kXBytes + kWBytes];
   // XCD-aware order in groups of kGroupM token blocks: consecutive tiles of one
   // XCD walk the group's token blocks for one channel block, then the next
-  // channel block, so the workgroups resident on an XCD at once share a few
-  // token blocks and a few weight blocks in its L2 (16 blocks: 0.47 ms against
-  // 0.59 ms for whole rows of channel blocks at 38,720 x 3072 x 3072)
-  constexpr int64_t kGroupM = 16;
+  // channel block, so the 32 workgroups resident on an XCD at once share 4
+  // token blocks and 8 weight blocks in its L2 (at 38,720 x 3072 x 3072: 0.458
+  // ms with 4 blocks per group; 2, 8 and 16: 0.467, 0.462 and 0.469 ms)
+  constexpr int64_t kGroupM = 4;
   const int64_t n_m = (a.M + kTM - 1) / kTM;
   const int64_t n_tiles = n_m * a.tiles_n;
   const int64_t tile = xcd_remap(blockIdx.x, n_tiles);
@@ -119,36 +120,34 @@ int8_linear_kernel(LinearArgs a) {
   const int64_t m0 = tm * kTM, n0 = tn * kTN;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave & 3, wn = wave >> 2;
 
-  // copies: the 8 KiB token tile is 8 units of 1 KiB (16 rows each), the 16 KiB
-  // weight tile 16 units; a wavefront copies 2 + 4 units per ring step.  Lane l
-  // lands at row 16 u + l / 4, chunk l % 4 of its unit and loads the chunk that
-  // the swizzle puts there.
+  // copies: each 16 KiB tile is 16 units of 1 KiB (16 rows each); a wavefront
+  // copies 2 + 2 units per ring step.  Lane l lands at row 16 u + l / 4, chunk
+  // l % 4 of its unit and loads the chunk that the swizzle puts there.
   const int64_t rows_x = a.M - m0 < kTM ? a.M - m0 : kTM;
   const int8_t* xb = a.x + m0 * a.K;
   const int8_t* wb = a.w + n0 * a.K;
   const int xbytes = static_cast<int>(rows_x * a.K), wbytes = static_cast<int>(kTN * a.K);
-  uint32_t xoff[2], woff[4];
+  uint32_t off[2];  // the same rows of both tiles
 #pragma unroll
   for (int i = 0; i < 2; ++i) {
     const int r = (wave * 2 + i) * 16 + lane / 4;
-    xoff[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
+    off[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
   }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int r = (wave * 4 + i) * 16 + lane / 4;
-    woff[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
-  }
+  const int steps = static_cast<int>(a.K / kKS);
   auto stage = [&](int s, char* dst) __attribute__((always_inline)) {
-    const int k0 = s * kKS;  // past the last step: re-copy step 0 (never read)
+    // past the last step: empty ranges, nothing is read (the slot is never read)
+    const bool live = s < steps;
+    const int k0 = live ? s * kKS : 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) dma16(xb, xbytes, xoff[i], k0, dst + (wave * 2 + i) * 1024);
+    for (int i = 0; i < 2; ++i)
+      dma16(xb, live ? xbytes : 0, off[i], k0, dst + (wave * 2 + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      dma16(wb, wbytes, woff[i], k0, dst + kXBytes + (wave * 4 + i) * 1024);
+    for (int i = 0; i < 2; ++i)
+      dma16(wb, live ? wbytes : 0, off[i], k0, dst + kXBytes + (wave * 2 + i) * 1024);
   };
-  constexpr int kOps = 6;
+  constexpr int kOps = 4;
 
   // operand read offsets: row r of a tile, chunk c = 2 ks + lane half
   const int hf = lane >> 5, li = lane & 31;
@@ -176,19 +175,18 @@ int8_linear_kernel(LinearArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
-  const int steps = static_cast<int>(a.K / kKS);
   stage(0, s_0);
-  stage(steps > 1 ? 1 : 0, s_1);
+  __builtin_amdgcn_sched_barrier(0);  // step 0's copies stay older than step 1's
+  stage(1, s_1);
   auto compute = [&](const char* tile, int s_fill, char* fill) __attribute__((always_inline)) {
-    v4i xf[2][2], wf[4][2];
+    v4i xf[2][2], wf[2][4];
 #pragma unroll
-    for (int tmi = 0; tmi < 2; ++tmi)
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) xf[tmi][ks] = *reinterpret_cast<const v4i*>(tile + xo[tmi][ks]);
-#pragma unroll
-    for (int tni = 0; tni < 4; ++tni)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) wf[tni][ks] = *reinterpret_cast<const v4i*>(tile + wo[tni][ks]);
+      for (int i = 0; i < 4; ++i) {
+        if (i < 2) xf[ks][i] = *reinterpret_cast<const v4i*>(tile + xo[i][ks]);
+        wf[ks][i] = *reinterpret_cast<const v4i*>(tile + wo[i][ks]);
+      }
     stage(s_fill, fill);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
@@ -196,20 +194,27 @@ int8_linear_kernel(LinearArgs a) {
       for (int tni = 0; tni < 4; ++tni)
 #pragma unroll
         for (int tmi = 0; tmi < 2; ++tmi)
-          acc[tni][tmi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[tni][ks], xf[tmi][ks],
+          acc[tni][tmi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ks][tni], xf[ks][tmi],
                                                                 acc[tni][tmi], 0, 0, 0);
+    // the ks = 0 operands first, then each MFMA with one ks = 1 read or one copy
+    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i >= 6 && i < 6 + kOps) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+    }
   };
   // ring: step j lives in slot j % 3; the copies of step j + 2 go out while
-  // step j is computed (steps past the end re-copy step 0 so every
-  // wavefront always has kOps copies per step in flight)
+  // step j is computed, so every wavefront has kOps copies per step in flight
   // (the host keeps the step count a multiple of 3)
   for (int j = 0; j < steps; j += 3) {
     qkv_wait_barrier<kOps>();
-    compute(s_0, j + 2 < steps ? j + 2 : 0, s_2);
+    compute(s_0, j + 2, s_2);
     qkv_wait_barrier<kOps>();
-    compute(s_1, j + 3 < steps ? j + 3 : 0, s_0);
+    compute(s_1, j + 3, s_0);
     qkv_wait_barrier<kOps>();
-    compute(s_2, j + 4 < steps ? j + 4 : 0, s_1);
+    compute(s_2, j + 4, s_1);
   }
   __builtin_amdgcn_s_waitcnt(qkv_vmcnt(0));
 
