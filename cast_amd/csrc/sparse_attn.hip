@@ -90,6 +90,7 @@ __device__ __forceinline__ int64_t out_row(const AttnArgs& a, int64_t r) {
 }
 
 constexpr float kTau = 8.0f;               // lazy-rescale threshold, log2 units
+constexpr float kTauPow = 256.0f;          // 2^kTau
 constexpr float kMagicF = 12582912.0f;     // 1.5 * 2^23
 constexpr int kMagicI = 0x4B400000;        // its fp32 bit pattern
 
@@ -625,43 +626,57 @@ sparse_attn_kernel(AttnArgs a) {
         for (int r = 0; r < 16; ++r)
           rv[t][r] = ((bits >> (16 * t + r)) & 1u) ? rv[t][r] : -INFINITY;
     }
-    float rmax = -INFINITY;
-#pragma unroll
-    for (int t = 0; t < C::KT; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, rv[t][r]);
-    rmax = pair_max(rmax);  // with the partner lane (lane ^ 32)
     const float c = INT8 ? a.scale_log2 * qs * kscale : a.scale_log2;
-    const float m_blk = (rmax == -INFINITY) ? -INFINITY
-                        : (INT8 ? (rmax - kMagicF) * c : rmax * c);
-    // lazy rescale: move the running max only when it grows by > 2^kTau
-    if (__ballot(m_blk > m_run + kTau) != 0) {  // wavefront-uniform
-      const float m_new = fmaxf(m_run, m_blk);
-      const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
-      l_run *= alpha;
-#pragma unroll
-      for (int dt = 0; dt < C::NDT; ++dt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
-      m_run = m_new;
-    }
-    const float bias = -(INT8 ? c * kMagicF : 0.0f) - (m_run == -INFINITY ? 0.0f : m_run);
     // Row sums add the fp32 exponentials in four independent chains: the
     // bf16 dot instruction would share the matrix pipe and stall behind the
     // other wavefront's MFMAs, plain adds issue beside them.
     v8bf p_op[C::KT][2];
-    float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto exps = [&]() __attribute__((always_inline)) -> float {
+      const float bias = -(INT8 ? c * kMagicF : 0.0f) - (m_run == -INFINITY ? 0.0f : m_run);
+      float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int t = 0; t < C::KT; ++t)
+      for (int t = 0; t < C::KT; ++t)
 #pragma unroll
-      for (int u = 0; u < 2; ++u)
+        for (int u = 0; u < 2; ++u)
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-          const float e = __builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + jj], c, bias));
-          p_op[t][u][jj] = static_cast<__bf16>(e);
-          lsum[jj & 3] += e;
-        }
-    l_run += (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+          for (int jj = 0; jj < 8; ++jj) {
+            const float e = __builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + jj], c, bias));
+            p_op[t][u][jj] = static_cast<__bf16>(e);
+            lsum[jj & 3] += e;
+          }
+      return (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
+    };
+    // Exponentials against the running max first.  Every term is >= 0, so a
+    // lane's partial sum bounds each of its terms: at most 2^kTau means none
+    // of its keys exceeds the running max by more than kTau, and the running
+    // max stays (lazy rescale).  Only otherwise, or while a row has no max yet,
+    // is the block max reduced (wavefront-uniform branch) and the running max
+    // moved, and the exponentials are taken again.  Steady blocks skip the
+    // serial max reduction before the first exponential.
+    float part = exps();
+    if (__ballot(m_run == -INFINITY || !(part <= kTauPow)) != 0) {
+      float rmax = -INFINITY;
+#pragma unroll
+      for (int t = 0; t < C::KT; ++t)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, rv[t][r]);
+      rmax = pair_max(rmax);  // with the partner lane (lane ^ 32)
+      const float m_blk = (rmax == -INFINITY) ? -INFINITY
+                          : (INT8 ? (rmax - kMagicF) * c : rmax * c);
+      // lazy rescale: move the running max only when it grows by > 2^kTau
+      if (__ballot(m_blk > m_run + kTau) != 0) {  // wavefront-uniform
+        const float m_new = fmaxf(m_run, m_blk);
+        const float alpha = m_new == -INFINITY ? 1.0f : __builtin_amdgcn_exp2f(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < C::NDT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o_acc[dt][r] *= alpha;
+        m_run = m_new;
+        part = exps();
+      }
+    }
+    l_run += part;
     if constexpr (kDmaInPv) {
       if constexpr (kValidCopy) stage_valid_flat(n_fill, fill);
       stage_flat(n_fill, fill, fill_tok);
