@@ -633,7 +633,7 @@ sparse_attn_kernel(AttnArgs a) {
     v8bf p_op[C::KT][2];
     auto exps = [&]() __attribute__((always_inline)) -> float {
       const float bias = -(INT8 ? c * kMagicF : 0.0f) - (m_run == -INFINITY ? 0.0f : m_run);
-      float lsum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      float lsum[4];  // seeded with the first four terms (0 + e cannot be folded)
 #pragma unroll
       for (int t = 0; t < C::KT; ++t)
 #pragma unroll
@@ -642,7 +642,8 @@ sparse_attn_kernel(AttnArgs a) {
           for (int jj = 0; jj < 8; ++jj) {
             const float e = __builtin_amdgcn_exp2f(fmaf(rv[t][8 * u + jj], c, bias));
             p_op[t][u][jj] = static_cast<__bf16>(e);
-            lsum[jj & 3] += e;
+            if (t == 0 && u == 0 && jj < 4) lsum[jj] = e;
+            else lsum[jj & 3] += e;
           }
       return (lsum[0] + lsum[1]) + (lsum[2] + lsum[3]);
     };
