@@ -205,11 +205,20 @@ def router_call(seed: int, iters: int) -> dict:
     for _ in range(3):
         router.refine(**kw)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(iters):
-        router.refine(**kw)
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / iters
+    # wall clock with the garbage collector paused, as timeit does: one full
+    # collection over the process's objects takes tens of ms, longer than the
+    # whole timed loop
+    import gc
+    gc.collect()
+    gc.disable()
+    try:
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            router.refine(**kw)
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / iters
+    finally:
+        gc.enable()
     return {"ms_per_refine": ms, "swap_count": rec["swap_count"],
             "candidates": rec["candidate_max"], "blocks": N, "heads": H}
 
