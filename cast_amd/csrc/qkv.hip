@@ -23,10 +23,7 @@ namespace rcsa {
 
 constexpr int kQThreads = 256;       // quantiser: 4 rows per workgroup
 constexpr int kGemmThreads = 512;    // 8 wavefronts: 4 (tokens) x 2 (channels)
-constexpr int kTM = 256, kTN = 256;  // workgroup tile (tokens x channels)
 constexpr int kKS = 64;              // bytes of K per ring step
-constexpr int kXBytes = kTM * kKS;   // 16 KiB
-constexpr int kWBytes = kTN * kKS;   // 16 KiB
 
 template <typename T>
 __device__ __forceinline__ float to_f32(T v) {
@@ -73,7 +70,9 @@ struct LinearArgs {
   const u16* bias;      // [N] bf16 or NULL
   u16* out;             // [M, ldo] bf16
   int64_t M, N, K, ldo;
-  int64_t tiles_n;      // N / kTN
+  // one launch: 256 x 256 tiles over rows [0, big_rows) on the first big_grid
+  // workgroups, then 128 x 128 tiles over rows [big_rows, M)
+  int64_t big_rows, big_grid;
 };
 
 constexpr int kQkvRsrc3 = 0x00020000;  // raw untyped buffer, 32-bit data format
@@ -99,40 +98,36 @@ __device__ __forceinline__ void qkv_wait_barrier() {
   asm volatile("s_waitcnt vmcnt(%0)\n\ts_barrier" ::"n"(N) : "memory");
 }
 
-__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
-int8_linear_kernel(LinearArgs a) {
-  __shared__ __attribute__((aligned(1024))) char s_0[kXBytes + kWBytes];
-  __shared__ __attribute__((aligned(1024))) char s_1[kXBytes + kWBytes];
-  __shared__ __attribute__((aligned(1024))) char s_2[kXBytes + kWBytes];
-  // XCD-aware order in groups of kGroupM token blocks: consecutive tiles of one
-  // XCD walk the group's token blocks for one channel block, then the next
-  // channel block, so the 32 workgroups resident on an XCD at once share 4
-  // token blocks and 8 weight blocks in its L2 (at 38,720 x 3072 x 3072: 0.458
-  // ms with 4 blocks per group; 2, 8 and 16: 0.467, 0.462 and 0.469 ms)
-  constexpr int64_t kGroupM = 4;
-  const int64_t n_m = (a.M + kTM - 1) / kTM;
-  const int64_t n_tiles = n_m * a.tiles_n;
-  const int64_t tile = xcd_remap(blockIdx.x, n_tiles);
-  if (tile < 0) return;
-  const int64_t group = tile / (kGroupM * a.tiles_n), in_group = tile % (kGroupM * a.tiles_n);
-  const int64_t group_m = n_m - group * kGroupM < kGroupM ? n_m - group * kGroupM : kGroupM;
-  const int64_t tm = group * kGroupM + in_group % group_m, tn = in_group / group_m;
-  const int64_t m0 = tm * kTM, n0 = tn * kTN;
+// A workgroup tile of 8 wavefronts (4 along tokens x 2 along channels), each
+// TMT x TNT tiles of 32 x 32.
+template <int TMT, int TNT>
+struct LinTile {
+  static constexpr int BM = 4 * 32 * TMT, BN = 2 * 32 * TNT;
+  static constexpr int XB = BM * kKS, WB = BN * kKS;          // bytes of a ring step
+  static constexpr int XU = BM / 16 / 8, WU = BN / 16 / 8;    // 1 KiB copy units per wavefront
+  static constexpr int OPS = XU + WU;                         // copies per wavefront and step
+  static_assert(XU == WU && XU >= 1, "both tiles are copied by the same rows");
+};
+
+template <int TMT, int TNT>
+__device__ __forceinline__ void linear_tile(const LinearArgs& a, int64_t m0, int64_t n0,
+                                            char* s_0, char* s_1, char* s_2) {
+  using T = LinTile<TMT, TNT>;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int wm = wave & 3, wn = wave >> 2;
 
-  // copies: each 16 KiB tile is 16 units of 1 KiB (16 rows each); a wavefront
-  // copies 2 + 2 units per ring step.  Lane l lands at row 16 u + l / 4, chunk
-  // l % 4 of its unit and loads the chunk that the swizzle puts there.
-  const int64_t rows_x = a.M - m0 < kTM ? a.M - m0 : kTM;
+  // copies: each tile is units of 1 KiB (16 rows each); a wavefront copies
+  // XU + WU units per ring step.  Lane l lands at row 16 u + l / 4, chunk l % 4
+  // of its unit and loads the chunk that the swizzle puts there.
+  const int64_t rows_x = a.M - m0 < T::BM ? a.M - m0 : T::BM;
   const int8_t* xb = a.x + m0 * a.K;
   const int8_t* wb = a.w + n0 * a.K;
-  const int xbytes = static_cast<int>(rows_x * a.K), wbytes = static_cast<int>(kTN * a.K);
-  uint32_t off[2];  // the same rows of both tiles
+  const int xbytes = static_cast<int>(rows_x * a.K), wbytes = static_cast<int>(T::BN * a.K);
+  uint32_t off[T::XU];  // the same rows of both tiles
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int r = (wave * 2 + i) * 16 + lane / 4;
+  for (int i = 0; i < T::XU; ++i) {
+    const int r = (wave * T::XU + i) * 16 + lane / 4;
     off[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
   }
   const int steps = static_cast<int>(a.K / kKS);
@@ -141,37 +136,36 @@ int8_linear_kernel(LinearArgs a) {
     const bool live = s < steps;
     const int k0 = live ? s * kKS : 0;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      dma16(xb, live ? xbytes : 0, off[i], k0, dst + (wave * 2 + i) * 1024);
+    for (int i = 0; i < T::XU; ++i)
+      dma16(xb, live ? xbytes : 0, off[i], k0, dst + (wave * T::XU + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
-      dma16(wb, live ? wbytes : 0, off[i], k0, dst + kXBytes + (wave * 2 + i) * 1024);
+    for (int i = 0; i < T::WU; ++i)
+      dma16(wb, live ? wbytes : 0, off[i], k0, dst + T::XB + (wave * T::WU + i) * 1024);
   };
-  constexpr int kOps = 4;
 
   // operand read offsets: row r of a tile, chunk c = 2 ks + lane half
   const int hf = lane >> 5, li = lane & 31;
-  int xo[2][2], wo[4][2];
+  int xo[TMT][2], wo[TNT][2];
 #pragma unroll
-  for (int tmi = 0; tmi < 2; ++tmi)
+  for (int tmi = 0; tmi < TMT; ++tmi)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int r = wm * 64 + tmi * 32 + li;
+      const int r = wm * 32 * TMT + tmi * 32 + li;
       xo[tmi][ks] = r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
     }
 #pragma unroll
-  for (int tni = 0; tni < 4; ++tni)
+  for (int tni = 0; tni < TNT; ++tni)
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const int r = wn * 128 + tni * 32 + li;
-      wo[tni][ks] = kXBytes + r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
+      const int r = wn * 32 * TNT + tni * 32 + li;
+      wo[tni][ks] = T::XB + r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
     }
 
-  v16i acc[4][2];
+  v16i acc[TNT][TMT];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < TNT; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < TMT; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
@@ -179,41 +173,42 @@ int8_linear_kernel(LinearArgs a) {
   __builtin_amdgcn_sched_barrier(0);  // step 0's copies stay older than step 1's
   stage(1, s_1);
   auto compute = [&](const char* tile, int s_fill, char* fill) __attribute__((always_inline)) {
-    v4i xf[2][2], wf[2][4];
+    v4i xf[2][TMT], wf[2][TNT];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (i < 2) xf[ks][i] = *reinterpret_cast<const v4i*>(tile + xo[i][ks]);
-        wf[ks][i] = *reinterpret_cast<const v4i*>(tile + wo[i][ks]);
-      }
+      for (int i = 0; i < TMT; ++i) xf[ks][i] = *reinterpret_cast<const v4i*>(tile + xo[i][ks]);
+#pragma unroll
+      for (int i = 0; i < TNT; ++i) wf[ks][i] = *reinterpret_cast<const v4i*>(tile + wo[i][ks]);
+    }
     stage(s_fill, fill);
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-      for (int tni = 0; tni < 4; ++tni)
+      for (int tni = 0; tni < TNT; ++tni)
 #pragma unroll
-        for (int tmi = 0; tmi < 2; ++tmi)
+        for (int tmi = 0; tmi < TMT; ++tmi)
           acc[tni][tmi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ks][tni], xf[ks][tmi],
                                                                 acc[tni][tmi], 0, 0, 0);
     // the ks = 0 operands first, then each MFMA with one ks = 1 read or one copy
-    __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+    constexpr int kReads = TMT + TNT;
+    __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
+    for (int i = 0; i < 2 * TMT * TNT; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i < 6) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (i >= 6 && i < 6 + kOps) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      if (i >= kReads && i < kReads + T::OPS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
     }
   };
   // ring: step j lives in slot j % 3; the copies of step j + 2 go out while
-  // step j is computed, so every wavefront has kOps copies per step in flight
+  // step j is computed, so every wavefront has OPS copies per step in flight
   // (the host keeps the step count a multiple of 3)
   for (int j = 0; j < steps; j += 3) {
-    qkv_wait_barrier<kOps>();
+    qkv_wait_barrier<T::OPS>();
     compute(s_0, j + 2, s_2);
-    qkv_wait_barrier<kOps>();
+    qkv_wait_barrier<T::OPS>();
     compute(s_1, j + 3, s_0);
-    qkv_wait_barrier<kOps>();
+    qkv_wait_barrier<T::OPS>();
     compute(s_2, j + 4, s_1);
   }
   __builtin_amdgcn_s_waitcnt(qkv_vmcnt(0));
@@ -221,16 +216,16 @@ int8_linear_kernel(LinearArgs a) {
   // epilogue: lane holds token m = li of each 32-token tile and channels
   // 8 g + 4 hf + (0..3) of each 32-channel tile
 #pragma unroll
-  for (int tmi = 0; tmi < 2; ++tmi) {
-    const int64_t m = m0 + wm * 64 + tmi * 32 + li;
+  for (int tmi = 0; tmi < TMT; ++tmi) {
+    const int64_t m = m0 + wm * 32 * TMT + tmi * 32 + li;
     if (m >= a.M) continue;
     const float xs = a.xs[m];
     u16* orow = a.out + m * a.ldo;
 #pragma unroll
-    for (int tni = 0; tni < 4; ++tni)
+    for (int tni = 0; tni < TNT; ++tni)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * 128 + tni * 32 + 8 * g + 4 * hf;
+        const int64_t n = n0 + wn * 32 * TNT + tni * 32 + 8 * g + 4 * hf;
         const float4 ws = *reinterpret_cast<const float4*>(a.ws + n);
         float y[4] = {static_cast<float>(acc[tni][tmi][4 * g + 0]) * xs * ws.x,
                       static_cast<float>(acc[tni][tmi][4 * g + 1]) * xs * ws.y,
@@ -246,6 +241,41 @@ int8_linear_kernel(LinearArgs a) {
         *reinterpret_cast<uint2*>(orow + n) =
             make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
       }
+  }
+}
+
+using BigTile = LinTile<2, 4>;    // 256 x 256, each wavefront 64 x 128
+using SmallTile = LinTile<1, 2>;  // 128 x 128, each wavefront 32 x 64
+
+__global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+int8_linear_kernel(LinearArgs a) {
+  __shared__ __attribute__((aligned(1024))) char s_0[BigTile::XB + BigTile::WB];
+  __shared__ __attribute__((aligned(1024))) char s_1[BigTile::XB + BigTile::WB];
+  __shared__ __attribute__((aligned(1024))) char s_2[BigTile::XB + BigTile::WB];
+  if (static_cast<int64_t>(blockIdx.x) < a.big_grid) {
+    // XCD-aware order in groups of kGroupM token blocks: consecutive tiles of
+    // one XCD walk the group's token blocks for one channel block, then the
+    // next channel block, so the 32 workgroups resident on an XCD at once share
+    // 4 token blocks and 8 weight blocks in its L2 (at 38,720 x 3072 x 3072:
+    // 0.458 ms with 4 blocks per group; 2, 8 and 16: 0.467, 0.462 and 0.469 ms)
+    constexpr int64_t kGroupM = 4;
+    const int64_t n_m = (a.big_rows + BigTile::BM - 1) / BigTile::BM;
+    const int64_t tiles_n = a.N / BigTile::BN;
+    const int64_t tile = xcd_remap(blockIdx.x, n_m * tiles_n);
+    if (tile < 0) return;
+    const int64_t group = tile / (kGroupM * tiles_n), in_group = tile % (kGroupM * tiles_n);
+    const int64_t group_m = n_m - group * kGroupM < kGroupM ? n_m - group * kGroupM : kGroupM;
+    const int64_t tm = group * kGroupM + in_group % group_m, tn = in_group / group_m;
+    linear_tile<2, 4>(a, tm * BigTile::BM, tn * BigTile::BN, s_0, s_1, s_2);
+  } else {
+    // the rows after big_rows in 128 x 128 tiles: they fill the last round,
+    // which whole 256 x 256 tiles would leave mostly idle
+    const int64_t n_m = (a.M - a.big_rows + SmallTile::BM - 1) / SmallTile::BM;
+    const int64_t tiles_n = a.N / SmallTile::BN;
+    const int64_t tile = xcd_remap(blockIdx.x - a.big_grid, n_m * tiles_n);
+    if (tile < 0) return;
+    const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
+    linear_tile<1, 2>(a, a.big_rows + tm * SmallTile::BM, tn * SmallTile::BN, s_0, s_1, s_2);
   }
 }
 
@@ -276,19 +306,35 @@ extern "C" int rcsa_int8_linear(const int8_t* x, const float* x_scale, const int
                                 const float* w_scale, const void* bias, int64_t M, int64_t N,
                                 int64_t K, void* out, int64_t ldo, hipStream_t stream) {
   if (!x || !x_scale || !w || !w_scale || !out) return RCSA_ERR_NULL;
-  if (M <= 0 || N <= 0 || K <= 0 || N % kTN || K % (3 * kKS) || ldo < N || ldo % 4)
+  if (M <= 0 || N <= 0 || K <= 0 || N % BigTile::BN || K % (3 * kKS) || ldo < N || ldo % 4)
     return RCSA_ERR_SHAPE;
   // the copies address a tile with 32-bit offsets
-  if (static_cast<int64_t>(kTN) * K >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
+  if (static_cast<int64_t>(BigTile::BM) * K >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
   if ((reinterpret_cast<uintptr_t>(x) & 15u) || (reinterpret_cast<uintptr_t>(w) & 15u) ||
       (reinterpret_cast<uintptr_t>(w_scale) & 15u) || (reinterpret_cast<uintptr_t>(out) & 7u) ||
       (reinterpret_cast<uintptr_t>(bias) & 7u))
     return RCSA_ERR_ALIGN;
+  // 256 x 256 tiles, except that a short last round (fewer tiles than half the
+  // compute units) is re-cut: the rows its tiles would cover go to 128 x 128
+  // tiles, a quarter of the work each, dispatched last to fill that round
+  const int64_t big_n = N / BigTile::BN;
+  const int64_t all_big = ((M + BigTile::BM - 1) / BigTile::BM) * big_n;
+  int64_t big_rows = M;
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+      cus > 0) {
+    const int64_t rem = all_big % cus;
+    const int64_t rows = (all_big - rem) / big_n * BigTile::BM;  // whole row blocks of full rounds
+    if (rem != 0 && 2 * rem < cus && rows > 0 && rows < M) big_rows = rows;
+  }
+  const int64_t big_tiles = ((big_rows + BigTile::BM - 1) / BigTile::BM) * big_n;
+  const int64_t small_tiles =
+      big_rows < M ? ((M - big_rows + SmallTile::BM - 1) / SmallTile::BM) * (N / SmallTile::BN) : 0;
+  if (big_tiles >= (int64_t{1} << 30) || small_tiles >= (int64_t{1} << 30)) return RCSA_ERR_SHAPE;
   LinearArgs a{x, x_scale, w, w_scale, static_cast<const u16*>(bias), static_cast<u16*>(out),
-               M, N, K, ldo, N / kTN};
-  const int64_t tiles = ((M + kTM - 1) / kTM) * a.tiles_n;
-  if (tiles >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
-  const dim3 grid(static_cast<unsigned>(xcd_grid(tiles)));
+               M, N, K, ldo, big_rows, xcd_grid(big_tiles)};
+  const dim3 grid(static_cast<unsigned>(a.big_grid + (small_tiles ? xcd_grid(small_tiles) : 0)));
   int8_linear_kernel<<<grid, dim3(kGemmThreads), 0, stream>>>(a);
   return launch_status();
 }

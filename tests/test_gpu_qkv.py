@@ -44,6 +44,25 @@ def test_int8_linear_matches_oracle(dev, M, with_bias):
     assert torch.equal(got.cpu(), orc.int8_linear(x, xs, w, ws, bias))
 
 
+def test_int8_linear_short_last_round(dev):
+    """5800 x 3072 x 192: 23 row blocks x 12 channel blocks of 256 x 256 tiles
+    leave a short last round on 256 compute units, so the last 424 rows run as
+    128 x 128 tiles (the last one 40 rows); every output element against the
+    oracle, bit for bit."""
+    from cast_amd import ops
+    g = torch.Generator().manual_seed(11)
+    M, N, K = 5800, 3072, 192
+    x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
+    w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
+    xs = torch.rand(M, generator=g) * 0.01 + 1e-4
+    ws = torch.rand(N, generator=g) * 0.01 + 1e-4
+    bias = torch.randn(N, generator=g).bfloat16()
+    print("int8 linear 5800 x 3072 x 192", flush=True)
+    got = ops.int8_linear(x.to(dev), xs.to(dev), w.to(dev), ws.to(dev), bias.to(dev))
+    torch.cuda.synchronize()
+    assert torch.equal(got.cpu(), orc.int8_linear(x, xs, w, ws, bias))
+
+
 def _int8_module(g, c_out, c_in, dev):
     w = torch.randint(-127, 128, (c_out, c_in), generator=g, dtype=torch.int8)
     return SimpleNamespace(in_features=c_in, out_features=c_out, weight_int8=w.to(dev),
@@ -63,7 +82,9 @@ def test_shared_qkv_matrix_shape(dev):
     outs = shared_int8_qkv(*mods, x.to(dev))
     torch.cuda.synchronize()
     rows = torch.randperm(L, generator=g)[:48].sort().values
-    rows = torch.cat([rows, torch.tensor([0, L - 1])])
+    # and the rows at 128-row boundaries of the last 640 rows
+    edge = [L - d for d in (640, 577, 576, 513, 512, 385, 384, 257, 256, 129, 128, 65, 64, 1)]
+    rows = torch.unique(torch.cat([rows, torch.tensor([0] + edge)]))
     xq, xs = orc.quantize_rows_int8(x[0, rows])
     for m, o in zip(mods, outs):
         assert o.shape == (1, L, C) and o.dtype == torch.bfloat16
