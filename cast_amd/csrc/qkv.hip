@@ -12,7 +12,8 @@
 // stores).  Both operands are staged by direct-to-LDS copies through a 3-slot
 // ring of 64-byte K steps (32 KiB per slot); 16-byte chunks of each 64-byte row
 // are XORed by (row / 4) mod 4 so the ds_read_b128 operand reads are conflict
-// free.
+// free.  When the 256 x 256 tiles would end in a short round, the rows of that
+// round run as 128 x 128 tiles (each wavefront 32 x 64) of the same launch.
 #include <type_traits>
 
 #include "rcsa_common.h"
