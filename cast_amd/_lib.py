@@ -1,7 +1,11 @@
-"""ctypes binding of the C ABI declared in ``include/rcsa.h``.
+"""Bindings of the C ABI declared in ``include/rcsa.h``.
 
-The shared library is built in-tree by ``cast_amd.build``.  There is no
-fallback: every operator raises if the library is missing or a call fails.
+``load()`` is the ctypes binding of ``librcsa.so``; ``torch_ops()`` loads the
+PyTorch-ROCm extension ``librcsa_torch.so`` (torch custom ops ``torch.ops.rcsa``
+over the same C ABI, used for the layer call's entry points) and binds it to
+the library ``load()`` opened.  Both are built in-tree by ``cast_amd.build``.
+There is no fallback: every operator raises if a library is missing or a call
+fails.
 """
 from __future__ import annotations
 
@@ -10,6 +14,7 @@ from ctypes import c_float, c_int, c_int64, c_void_p
 from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "librcsa.so"
+TORCH_OPS_PATH = Path(__file__).resolve().parent / "_lib" / "librcsa_torch.so"
 
 RCSA_OK = 0
 RCSA_BF16 = 0
@@ -88,6 +93,27 @@ def load() -> ctypes.CDLL:
                       else c_int)
     _lib = lib
     return lib
+
+
+_torch_ops = None
+
+
+def torch_ops():
+    """``torch.ops.rcsa``: the extension's custom ops, bound to ``LIB_PATH``."""
+    global _torch_ops
+    if _torch_ops is not None:
+        return _torch_ops
+    load()
+    if not TORCH_OPS_PATH.exists():
+        raise RuntimeError(
+            f"RCSA torch extension not built: {TORCH_OPS_PATH} is missing "
+            "(run `python -m cast_amd.build`)"
+        )
+    import torch
+    torch.ops.load_library(str(TORCH_OPS_PATH))
+    torch.ops.rcsa.bind_library(str(LIB_PATH))
+    _torch_ops = torch.ops.rcsa
+    return _torch_ops
 
 
 def check(status: int, fn: str) -> None:

@@ -123,8 +123,38 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, out)
+    ext = build_torch_ops()
     if verbose:
-        print(f"built {out} from {len(sources)} sources")
+        print(f"built {out} from {len(sources)} sources and {ext.name}")
+    return out
+
+
+TORCH_OPS = "librcsa_torch.so"
+
+
+def build_torch_ops() -> Path:
+    """Compile ``csrc/torch_ops.cpp`` (the PyTorch-ROCm extension: torch custom
+    ops over the C ABI) into ``_lib/librcsa_torch.so`` against this torch."""
+    import torch
+    import torch.utils.cpp_extension as ce
+
+    src = CSRC / "torch_ops.cpp"
+    out = LIBDIR / TORCH_OPS
+    tmp = LIBDIR / (TORCH_OPS + ".tmp")
+    rocm = os.environ.get("ROCM_PATH", "/opt/rocm")
+    libdirs = ce.library_paths()
+    cmd = [shutil.which("g++") or "g++", "-O2", "-std=c++17", "-fPIC", "-shared",
+           "-D__HIP_PLATFORM_AMD__=1", "-DUSE_ROCM=1",
+           f"-D_GLIBCXX_USE_CXX11_ABI={int(torch._C._GLIBCXX_USE_CXX11_ABI)}",
+           *[f"-I{p}" for p in ce.include_paths()], f"-I{rocm}/include",
+           str(src), "-o", str(tmp),
+           *[f"-L{p}" for p in libdirs], "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu",
+           f"-L{rocm}/lib", "-lamdhip64", "-ldl",
+           *[f"-Wl,-rpath,{p}" for p in libdirs], f"-Wl,-rpath,{rocm}/lib"]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"torch_ops.cpp failed:\n{res.stderr[-4000:]}")
+    os.replace(tmp, out)
     return out
 
 

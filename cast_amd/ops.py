@@ -197,13 +197,10 @@ def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Te
     else:
         q_i8 = q_scale = ksum = kmin = kmax = None
     mask = torch.empty(NK, block_size // 32, device=k.device, dtype=torch.int32)
-    st = _lib.load().rcsa_pool_query_key(
-        q.data_ptr(), k.data_ptr(), code, B, H, NQ, NK, block_size, D, *q_strides, *k_strides,
-        _ptr(qv), _ptr(kv), _ptr(qm), q_src, _ptr(km), k_src,
-        qhat.data_ptr(), _ptr(q_i8), _ptr(q_scale),
-        khat.data_ptr(), _ptr(ksum), _ptr(kmin), _ptr(kmax), mask.data_ptr(),
-        _stream())
-    check(st, fn)
+    # through the torch extension (rcsa::pool_query_key -> rcsa_pool_query_key)
+    _lib.torch_ops().pool_query_key(
+        q, k, code, [B, H, NQ, NK, block_size, D], list(q_strides), list(k_strides),
+        qv, kv, qm, q_src, km, k_src, qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask)
     return qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask
 
 
@@ -412,12 +409,11 @@ def quantize_key_select(k, valid, block_size, ksum, kmin, kmax, qhat, khat, k_se
     score = torch.empty(nbh, nq, NB, device=k.device, dtype=torch.float32)
     indices = torch.empty(nbh, nq, max_k, device=k.device, dtype=torch.int32)
     counts = torch.empty(nbh, nq, device=k.device, dtype=torch.int32)
-    check(_lib.load().rcsa_quantize_key_select(
-        k.data_ptr(), code, B, H, NB, block_size, D, *strides, _ptr(v), _ptr(sm), src_len,
-        ksum.data_ptr(), kmin.data_ptr(), kmax.data_ptr(), kmean.data_ptr(), k_i8.data_ptr(),
-        k_scale.data_ptr(), qhat.data_ptr(), khat.data_ptr(), nq, score.data_ptr(),
-        _ptr(row_k), stride, k_fixed, _ptr(fm), _ptr(am), mstride, indices.data_ptr(), max_k,
-        counts.data_ptr(), _stream()), fn)
+    # through the torch extension (rcsa::quantize_key_select -> rcsa_quantize_key_select)
+    _lib.torch_ops().quantize_key_select(
+        k, code, [B, H, NB, block_size, D], list(strides), v, sm, src_len, ksum, kmin, kmax,
+        kmean, k_i8, k_scale, qhat, khat, nq, score, row_k, stride, k_fixed, fm, am, mstride,
+        indices, max_k, counts)
     return k_i8, k_scale, kmean, score, indices, counts
 
 
@@ -583,18 +579,13 @@ def sparse_attn_bf16(q, k, v, indices, counts, valid=None, *, block_m=128, block
     lse = torch.empty(B, H, n_rows, device=q.device, dtype=torch.float32) if return_lse else None
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q.device, fn)
-    st = _lib.load().rcsa_sparse_attn_bf16_split(
-        q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(kv), _ptr(block_mask), scale, _ptr(lse),
-        out.data_ptr(),
-        indices.data_ptr(), counts.data_ptr(),
-        *_bhld_strides(q, gathered), *_bhld_strides(k, gathered), *_bhld_strides(v, gathered),
-        *_bhld_strides(out, gathered),
-        indices.stride(0), indices.stride(1), indices.stride(2),
-        counts.stride(0), counts.stride(1), counts.stride(2),
-        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes,
-        _ptr(qm), n_qtok, _ptr(km), n_ktok, _ptr(om), n_out if om is not None else 0,
-        _stream())
-    check(st, fn)
+    # through the torch extension (rcsa::sparse_attn_bf16 -> rcsa_sparse_attn_bf16_split)
+    _lib.torch_ops().sparse_attn_bf16(
+        q, k, v, kv, block_mask, scale, lse, out, indices, counts,
+        [B, H, Lq, Lk, D, block_m, block_n, indices.shape[3]],
+        [*_bhld_strides(q, gathered), *_bhld_strides(k, gathered), *_bhld_strides(v, gathered),
+         *_bhld_strides(out, gathered), *indices.stride()[:3], *counts.stride()[:3]],
+        ns, ws, qm, n_qtok, km, n_ktok, om, n_out if om is not None else 0)
     return (out, lse) if return_lse else out
 
 
@@ -668,18 +659,14 @@ def sparse_attn_int8(q_i8, q_scale, k_i8, k_scale, v, indices, counts, valid=Non
                        dtype=torch.float32) if return_lse else None)
     scale = 1.0 / math.sqrt(D) if sm_scale is None else float(sm_scale)
     ns, ws, nbytes = _split_plan(B, H, Lq, D, block_m, indices.shape[3], n_split, q_i8.device, fn)
-    st = _lib.load().rcsa_sparse_attn_int8_split(
-        q_i8.data_ptr(), q_scale.data_ptr(), q_scale.shape[1], k_i8.data_ptr(),
-        k_scale.data_ptr(), k_scale.shape[1], v.data_ptr(), _ptr(kv), _ptr(block_mask),
-        scale, _ptr(lse),
-        out.data_ptr(), indices.data_ptr(), counts.data_ptr(),
-        q_i8.stride(0), q_i8.stride(1), q_i8.stride(2),
-        k_i8.stride(0), k_i8.stride(1), k_i8.stride(2), *v_strides, *o_strides,
-        indices.stride(0), indices.stride(1), indices.stride(2),
-        counts.stride(0), counts.stride(1), counts.stride(2),
-        B, H, Lq, Lk, D, block_m, block_n, indices.shape[3], ns, _ptr(ws), nbytes, _ptr(om),
-        n_out, _ptr(vm), v_rows, _stream())
-    check(st, fn)
+    # through the torch extension (rcsa::sparse_attn_int8 -> rcsa_sparse_attn_int8_split)
+    _lib.torch_ops().sparse_attn_int8(
+        q_i8, q_scale, q_scale.shape[1], k_i8, k_scale, k_scale.shape[1], v, kv, block_mask,
+        scale, lse, out, indices, counts,
+        [B, H, Lq, Lk, D, block_m, block_n, indices.shape[3]],
+        [*q_i8.stride()[:3], *k_i8.stride()[:3], *v_strides, *o_strides,
+         *indices.stride()[:3], *counts.stride()[:3]],
+        ns, ws, om, n_out, vm, v_rows)
     return (out, lse) if return_lse else out
 
 
@@ -799,8 +786,7 @@ def quantize_rows_int8(x: torch.Tensor):
     M, C = x2.shape
     q = torch.empty(M, C, device=x.device, dtype=torch.int8)
     scale = torch.empty(M, device=x.device, dtype=torch.float32)
-    check(_lib.load().rcsa_quantize_rows_int8(x2.data_ptr(), code, M, C, x2.stride(0),
-                                              q.data_ptr(), scale.data_ptr(), _stream()), fn)
+    _lib.torch_ops().quantize_rows_int8(x2, code, q, scale)
     return q, scale
 
 
@@ -829,7 +815,5 @@ def int8_linear(x_i8: torch.Tensor, x_scale: torch.Tensor, w_i8: torch.Tensor,
         out = torch.empty(M, N, device=x_i8.device, dtype=torch.bfloat16)
     if out.dtype != torch.bfloat16 or out.shape != (M, N) or out.stride(1) != 1:
         raise ValueError(f"{fn}: out must be bfloat16 [{M}, {N}] with contiguous rows")
-    check(_lib.load().rcsa_int8_linear(x_i8.data_ptr(), xs.data_ptr(), w_i8.data_ptr(),
-                                       ws.data_ptr(), _ptr(b), M, N, K, out.data_ptr(),
-                                       out.stride(0), _stream()), fn)
+    _lib.torch_ops().int8_linear(x_i8, xs, w_i8, ws, b, out)
     return out

@@ -48,6 +48,49 @@ def test_status_strings_and_version(lib):
         _lib.check(2, "rcsa_demo")
 
 
+TORCH_OPS = {
+    "pool_query_key": "rcsa_pool_query_key",
+    "quantize_key_select": "rcsa_quantize_key_select",
+    "sparse_attn_bf16": "rcsa_sparse_attn_bf16_split",
+    "sparse_attn_int8": "rcsa_sparse_attn_int8_split",
+    "quantize_rows_int8": "rcsa_quantize_rows_int8",
+    "int8_linear": "rcsa_int8_linear",
+}
+
+
+@pytest.fixture(scope="module")
+def rcsa_ops(lib):
+    if not _lib.TORCH_OPS_PATH.exists():
+        from cast_amd import build
+        build.build_torch_ops()
+    return _lib.torch_ops()
+
+
+def test_torch_extension_registers_the_ops(rcsa_ops):
+    declared = set(_header_functions())
+    for op, entry in TORCH_OPS.items():
+        assert entry in declared
+        schema = str(getattr(rcsa_ops, op).default._schema)
+        assert schema.startswith(f"rcsa::{op}("), schema
+        assert schema.endswith("-> ()"), schema  # outputs are written in place
+    # outputs are declared mutated, inputs are not
+    schema = str(rcsa_ops.int8_linear.default._schema)
+    assert "Tensor(a!) out" in schema and "Tensor x_i8," in schema
+
+
+def test_torch_ops_refuse_host_tensors(rcsa_ops):
+    x = torch.zeros(4, 256, dtype=torch.int8)
+    xs = torch.ones(4)
+    with pytest.raises(RuntimeError, match=r"int8_linear: .* must be a GPU tensor"):
+        rcsa_ops.int8_linear(x, xs, x, xs, None, torch.empty(4, 4, dtype=torch.bfloat16))
+    q = torch.zeros(1, 1, 128, 128, dtype=torch.bfloat16)
+    idx = torch.zeros(1, 1, 1, 1, dtype=torch.int32)
+    cnt = torch.ones(1, 1, 1, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match=r"sparse_attn_bf16: dims needs 8 values"):
+        rcsa_ops.sparse_attn_bf16(q, q, q, None, None, 1.0, None, q, idx, cnt, [1], [0] * 18, 1,
+                                  None, None, 0, None, 0, None, 0)
+
+
 def test_ops_refuse_host_tensors():
     q = torch.zeros(1, 1, 128, 128, dtype=torch.bfloat16)
     with pytest.raises(RuntimeError, match="HIP device"):
