@@ -25,11 +25,12 @@ def _inputs(dev, seed=3, H=2, nqb=3, nkb=8, D=128, bs=128, max_k=4):
     return q, k, v, valid.to(dev), idx, cnt
 
 
-def _stub_call(q, k, v, key_valid, indices, counts, out, block_size):
+def _stub_call(q, k, v, key_valid, indices, counts, out, block_size, sm_scale=None):
     """The direct launch of the binding example: unsplit, no workspace, no maps."""
     B, H, Lq, D = q.shape
     torch.ops.rcsa.sparse_attn_bf16(
-        q, k, v, key_valid, None, 1.0 / math.sqrt(D), None, out, indices, counts,
+        q, k, v, key_valid, None, 1.0 / math.sqrt(D) if sm_scale is None else sm_scale, None,
+        out, indices, counts,
         [B, H, Lq, k.shape[2], D, block_size, block_size, indices.shape[3]],
         [*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3],
          *indices.stride()[:3], *counts.stride()[:3]],
@@ -80,6 +81,27 @@ def test_direct_op_rejects_bad_arguments(dev):
         w = torch.zeros(256, 384, dtype=torch.int8, device=dev)
         rcsa.int8_linear(x, torch.ones(4, device=dev), w, torch.ones(256, device=dev), None,
                          torch.empty(4, 256, dtype=torch.bfloat16, device=dev))
+    # dims that reach past a tensor are refused before any launch
+    with pytest.raises(RuntimeError, match=r"sparse_attn_bf16: k spans \d+ elements, the call "
+                                           r"reaches \d+"):
+        B, H, Lq, D = q.shape
+        ks = k[:, :, :512]
+        rcsa.sparse_attn_bf16(
+            q, ks, v, valid, None, 1.0 / math.sqrt(D), None, out, idx, cnt,
+            [B, H, Lq, k.shape[2], D, 128, 128, idx.shape[3]],
+            [*q.stride()[:3], *ks.stride()[:3], *v.stride()[:3], *out.stride()[:3],
+             *idx.stride()[:3], *cnt.stride()[:3]],
+            1, None, None, 0, None, 0, None, 0)
+    with pytest.raises(RuntimeError, match=r"sparse_attn_bf16: k_valid spans"):
+        _stub_call(q, k, v, valid[:100], idx, cnt, out, 128)
+    with pytest.raises(RuntimeError, match=r"sparse_attn_bf16: indices spans"):
+        B, H, Lq, D = q.shape
+        rcsa.sparse_attn_bf16(
+            q, k, v, valid, None, 1.0 / math.sqrt(D), None, out, idx, cnt,
+            [B, H, Lq, k.shape[2], D, 128, 128, idx.shape[3]],
+            [*q.stride()[:3], *k.stride()[:3], *v.stride()[:3], *out.stride()[:3],
+             idx.stride(0), idx.stride(1), 2 * idx.stride(2), *cnt.stride()[:3]],
+            1, None, None, 0, None, 0, None, 0)
     # a library status becomes the same RuntimeError form as the ctypes path
     with pytest.raises(RuntimeError, match=r"sparse_attn_bf16: .*\(status \d+\)"):
-        _stub_call(q, k, v, valid, idx, cnt, out, 96)  # no 96-token block shape
+        _stub_call(q, k, v, valid, idx, cnt, out, 128, sm_scale=0.0)  # refused by the library
