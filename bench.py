@@ -35,6 +35,9 @@ if ROOT not in sys.path:
 INT8_PEAK_TOPS = 5000.0     # MI355X dense int8 MFMA
 BF16_PEAK_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 HBM_PEAK_GBS = 8000.0       # MI355X HBM3E
+# QK^T on int8 and PV on bf16 take equal op counts (2 D per key and query row
+# each), so the attention's ceiling is the harmonic mean of the two peaks
+MIXED_CEILING_TOPS = 1.0 / (0.5 / INT8_PEAK_TOPS + 0.5 / BF16_PEAK_TFLOPS)
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "attn_int8_dit_traffic.txt")
 
 
@@ -501,8 +504,25 @@ def main() -> int:
                 layer_call(lw)
         torch.cuda.synchronize()
         step_ms = (time.perf_counter() - t0) * 1e3 / n_sweep
+        # per layer: the attention launch alone (HIP events), its ops and the
+        # fraction of the dense int8 peak and of the int8-QK + bf16-PV ceiling
+        per_layer = []
+        for p, lw in zip(plan, layers):
+            r = layer_call(lw)
+            ops_l = lw.attention_ops(r.indices, r.counts)
+            o = torch.empty_like(lw.q)
+            ms_l = _events_time(lambda: ops.sparse_attn_int8(
+                r.q_i8, r.q_scale, r.k_i8, r.k_scale, lw.v, r.indices, r.counts, None, out=o,
+                block_mask=r.k_mask), 10, 2)
+            tops = ops_l / ms_l / 1e9
+            per_layer.append({"query_frames": p["query_frames"], "fraction": p["fraction"],
+                              "attn_ms": round(ms_l, 4), "attn_TOPS": round(tops, 1),
+                              "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
+                              "frac_mixed_ceiling": round(tops / MIXED_CEILING_TOPS, 4)})
+            del r, o
         extras["step_sweep_30_layers"] = {"ms_per_step": step_ms,
-                                          "effective_TOPS": sweep_ops / step_ms / 1e9}
+                                          "effective_TOPS": sweep_ops / step_ms / 1e9,
+                                          "attention_per_layer": per_layer}
         del layers
         extras["compact_layout_call"] = compact_layout_call(args.seed, iters)
         # per-row budgets on the device: 30 layers x 28 query blocks, and one
