@@ -6,6 +6,8 @@
 
 namespace rcsa {
 
+static int64_t cus_per_xcd();
+
 template <bool INT8>
 static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
   const int64_t per_xcd = a.xcd_direct + (a.xcd_items - a.xcd_direct) * a.n_split;
@@ -22,6 +24,11 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
     return RCSA_ERR_SHAPE;
   if constexpr (INT8) {  // the validity-bits flavour of the 3-slot ring
     if (a.kmask != nullptr && D == 128 && BM == 128 && BN == 128) {
+      // at least two full rounds of query blocks per XCD: three 4-wavefront
+      // workgroups per compute unit (packed and gathered sources alike, so the
+      // two forms of a call stay bit-identical)
+      const int64_t cux = cus_per_xcd();
+      if (cux > 0 && a.xcd_items >= 2 * cux) return launch_int8_cu3(a, grid, a.kv_tok != nullptr, s);
       if (a.kv_tok != nullptr)
         sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true, true><<<grid, dim3(512), 0, s>>>(a);
       else

@@ -6,10 +6,12 @@
 //
 // Work decomposition: one workgroup = one (batch, head, query block) of
 // BLOCK_M rows; it streams only the key blocks named in its block list.
-// The workgroup has 2 * BLOCK_M / 32 wavefronts: row group rg (32 query
-// rows) x key half kh (BLOCK_N / 2 keys of every block).  The two key halves
-// keep independent online-softmax states that are merged once at the end, so
-// eight wavefronts share every staged tile (two per SIMD).
+// The workgroup has NKH * BLOCK_M / 32 wavefronts: row group rg (32 query
+// rows) x key half kh.  With NKH = 2 the two key halves keep independent
+// online-softmax states that are merged once at the end, so eight wavefronts
+// share every staged tile (two per SIMD, one workgroup per compute unit).
+// With NKH = 1 and WPE = 3 a workgroup of four wavefronts takes whole ring
+// steps and three workgroups share a compute unit.
 //
 // Staging: each selected K tile (row-major, 16-byte chunks XOR-swizzled) and
 // V tile (row-major, swizzled) is copied global -> LDS with direct-to-LDS
@@ -164,8 +166,10 @@ static __device__ uint8_t kAllValid[128] = {RCSA_ONES16, RCSA_ONES16, RCSA_ONES1
 #undef RCSA_ONES16
 
 // BNS keys of a block are staged per ring step (BN / BNS steps per selected
-// block); NKH key halves split every staged step between wavefronts.
-template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH>
+// block); NKH key halves split every staged step between wavefronts.  WPE > 0:
+// several workgroups share a compute unit, WPE waves per SIMD in all (a
+// register budget of 512 / WPE); 0: one workgroup per compute unit.
+template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH, int WPE = 0>
 struct AttnCfg {
   static constexpr int NRG = BM / 32;            // row groups
   static constexpr int NW = NRG * NKH;           // wavefronts: row group x key half
@@ -193,8 +197,10 @@ struct AttnCfg {
   static constexpr int MW = NDT * 16 * 64 + 128; // floats of one row group's merge partial
   static constexpr int MPER = (NRG + STAGES - 1) / STAGES;  // partials per slot
   // a 3-slot ring's slots are grown to hold the key-half merge partials (the
-  // 64-key bf16 ring: 2 x 16.5 KiB in each 32.25 KiB slot)
-  static constexpr int SLOT = (STAGES == 3 && MPER * MW * 4 > BUF + 256) ? MPER * MW * 4 : BUF + 256;
+  // 64-key bf16 ring: 2 x 16.5 KiB in each 32.25 KiB slot); workgroups that
+  // share a compute unit have one key half and no merge
+  static constexpr int SLOT = (WPE == 0 && STAGES == 3 && MPER * MW * 4 > BUF + 256)
+                                  ? MPER * MW * 4 : BUF + 256;
   static constexpr bool MERGE_IN_SLOTS = MPER * MW * 4 <= SLOT;
   // the vmcnt accounting of a 3-deep ring needs the same copy count on every wavefront
   static_assert(STAGES == 2 || (KUNITS % NW == 0 && VUNITS % NW == 0), "uneven copies");
@@ -202,6 +208,7 @@ struct AttnCfg {
   static_assert(STAGES == 2 || STAGES == 3, "ring depth");
   static_assert((NKH == 1 || NKH == 2) && HK % 32 == 0 && BN % BNS == 0, "key split");
   static_assert(BNS <= 256, "validity bytes of one step fit the slot tail");
+  static_assert(WPE == 0 || NKH == 1, "workgroups sharing a compute unit merge no key halves");
 };
 
 // Direct-to-LDS copy of 16 (4) bytes per lane through a buffer resource over
@@ -219,28 +226,19 @@ __device__ __forceinline__ void buffer_copy4(char* base, int bytes, uint32_t vof
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RCSA_LDS(void, dst), 4, voff, 0, 0, 0);
 }
 
-// Waves per SIMD the register budget is sized for.  A ring of BNS < BN keys
-// whose slots hold at most 80 KiB fits two workgroups in one compute unit's
-// LDS, so exactly two waves of each SIMD's share must fit; otherwise the
-// compiler's default range applies (at least the workgroup's own waves per SIMD).
-template <bool INT8, int D, int BN, int STAGES, int BNS>
-constexpr bool attn_two_wg() {
-  return BNS < BN && STAGES * BNS * (D * (INT8 ? 1 : 2) + 2 * D) <= 80 * 1024;
-}
-template <bool INT8, int D, int BN, int STAGES, int BNS, int NKH, int NT>
-constexpr int attn_waves_min() {
-  return attn_two_wg<INT8, D, BN, STAGES, BNS>() ? 2 * NKH : (NT / 256 > 1 ? NT / 256 : 1);
-}
-template <bool INT8, int D, int BN, int STAGES, int BNS, int NKH>
-constexpr int attn_waves_max() { return attn_two_wg<INT8, D, BN, STAGES, BNS>() ? 2 * NKH : 8; }
+// Waves per SIMD the register budget is sized for: WPE when several
+// workgroups share a compute unit, otherwise at least the workgroup's own.
+template <int NT, int WPE>
+constexpr int attn_waves_min() { return WPE > 0 ? WPE : (NT / 256 > 1 ? NT / 256 : 1); }
+template <int WPE>
+constexpr int attn_waves_max() { return WPE > 0 ? WPE : 8; }
 
 template <bool INT8, int D, int BM, int BN, int STAGES, int BNS, int NKH, bool MASK,
-          bool GATHER = false>
+          bool GATHER = false, int WPE = 0>
 __global__ void __launch_bounds__(BM * 2 * NKH)  // == AttnCfg::NT
-__attribute__((amdgpu_waves_per_eu(attn_waves_min<INT8, D, BN, STAGES, BNS, NKH, BM * 2 * NKH>(),
-                                   attn_waves_max<INT8, D, BN, STAGES, BNS, NKH>())))
+__attribute__((amdgpu_waves_per_eu(attn_waves_min<BM * 2 * NKH, WPE>(), attn_waves_max<WPE>())))
 sparse_attn_kernel(AttnArgs a) {
-  using C = AttnCfg<INT8, D, BM, BN, STAGES, BNS, NKH>;
+  using C = AttnCfg<INT8, D, BM, BN, STAGES, BNS, NKH, WPE>;
   typedef typename std::conditional<INT8, v4i, v8bf>::type OpT;
   // A 3-slot ring issues its copies between the PV MFMAs, every wavefront
   // the same kOps copies per ring step (validity bytes included)
@@ -968,6 +966,9 @@ attn_merge_kernel(AttnArgs a) {
 // the default instruction scheduler: the kernels of sparse_attn.hip are
 // scheduled for instruction-level parallelism, which makes this one slower.
 int launch_bf16_gather(AttnArgs& a, dim3 grid, hipStream_t s);
+// The int8 kernel with validity bits as three 4-wavefront workgroups per
+// compute unit (sparse_attn_int8_cu3.hip); `gather` selects the V slot-map form.
+int launch_int8_cu3(AttnArgs& a, dim3 grid, bool gather, hipStream_t s);
 
 }  // namespace rcsa
 
