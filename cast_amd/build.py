@@ -45,9 +45,13 @@ COMMON_FLAGS = [
 # Per-source flags.  The attention kernels are scheduled for instruction-level
 # parallelism (interleaved A/B on one MI355X: int8 attention 1.4%, bf16 1.7%,
 # the gathered int8 layer call 3.5% faster); the gathered bf16 kernel, 4.5%
-# slower that way, sits in a source of its own with the default scheduler.
+# slower that way, sits in a source of its own with the default scheduler, as
+# does the int8 kernel of three workgroups per compute unit (15% slower with
+# the ILP scheduler).  The gathered bf16 kernel of three workgroups per compute
+# unit fits its 168 VGPRs without spills only under the memory-clause scheduler.
 FILE_FLAGS = {
     "sparse_attn.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "sparse_attn_bf16_gather_cu3.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
 }
 
 

@@ -38,9 +38,16 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
   }
   if constexpr (!INT8) {  // bf16 at D 128: a 3-slot ring of 64-key steps (3 x 32 KiB)
     if (D == 128 && BM == 128 && BN == 128) {
+      // validity bits and at least two full rounds of query blocks per XCD:
+      // three 4-wavefront workgroups per compute unit, 32-key steps (3 x 16.25 KiB)
+      const int64_t cux = cus_per_xcd();
+      const bool cu3 = a.kmask != nullptr && cux > 0 && a.xcd_items >= 2 * cux;
       if (a.kv_tok != nullptr)
-        return launch_bf16_gather(a, grid, s);
-      if (a.kmask != nullptr)
+        return cu3 ? launch_bf16_gather_cu3(a, grid, s) : launch_bf16_gather(a, grid, s);
+      if (cu3)
+        sparse_attn_kernel<false, 128, 128, 128, 3, 32, 1, true, false, 3>
+            <<<grid, dim3(256), 0, s>>>(a);
+      else if (a.kmask != nullptr)
         sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, true><<<grid, dim3(512), 0, s>>>(a);
       else
         sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, false><<<grid, dim3(512), 0, s>>>(a);

@@ -966,6 +966,9 @@ attn_merge_kernel(AttnArgs a) {
 // the default instruction scheduler: the kernels of sparse_attn.hip are
 // scheduled for instruction-level parallelism, which makes this one slower.
 int launch_bf16_gather(AttnArgs& a, dim3 grid, hipStream_t s);
+// The same as three 4-wavefront workgroups per compute unit
+// (sparse_attn_bf16_gather_cu3.hip).
+int launch_bf16_gather_cu3(AttnArgs& a, dim3 grid, hipStream_t s);
 // The int8 kernel with validity bits as three 4-wavefront workgroups per
 // compute unit (sparse_attn_int8_cu3.hip); `gather` selects the V slot-map form.
 int launch_int8_cu3(AttnArgs& a, dim3 grid, bool gather, hipStream_t s);
