@@ -47,11 +47,12 @@ COMMON_FLAGS = [
 # the gathered int8 layer call 3.5% faster); the gathered bf16 kernel, 4.5%
 # slower that way, sits in a source of its own with the default scheduler, as
 # does the int8 kernel of three workgroups per compute unit (15% slower with
-# the ILP scheduler).  The gathered bf16 kernel of three workgroups per compute
-# unit fits its 168 VGPRs without spills only under the memory-clause scheduler.
+# the ILP scheduler).  The bf16 kernels of three workgroups per compute unit
+# with gathered sources or validity bytes fit their 168 VGPRs without spills
+# only under the memory-clause scheduler.
 FILE_FLAGS = {
     "sparse_attn.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
-    "sparse_attn_bf16_gather_cu3.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
+    "sparse_attn_bf16_cu3.hip": ["-mllvm", "-amdgpu-sched-strategy=max-memory-clause"],
 }
 
 

@@ -12,8 +12,7 @@ template <bool INT8>
 static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream_t s) {
   const int64_t per_xcd = a.xcd_direct + (a.xcd_items - a.xcd_direct) * a.n_split;
   const dim3 grid(static_cast<unsigned>(kNumXcd * per_xcd));
-  // int8 at D=128, 128x128 blocks keeps two blocks in flight (3 x 48 KiB);
-  // the other shapes double-buffer.
+  // the shapes other than D 128 with 128 x 128 blocks double-buffer
 #define RCSA_ATTN(D_, BM_, BN_, ST_)                                                   \
   if (D == D_ && BM == BM_ && BN == BN_) {                                              \
     sparse_attn_kernel<INT8, D_, BM_, BN_, ST_, BN_, 2, false><<<grid, dim3(BM_ * 4), 0, s>>>(a); \
@@ -22,39 +21,38 @@ static int launch_attn(AttnArgs& a, int64_t D, int64_t BM, int64_t BN, hipStream
   // gathered sources exist for the 3-slot rings with validity bits only
   if (a.kv_tok != nullptr && !(a.kmask != nullptr && D == 128 && BM == 128 && BN == 128))
     return RCSA_ERR_SHAPE;
-  if constexpr (INT8) {  // the validity-bits flavour of the 3-slot ring
-    if (a.kmask != nullptr && D == 128 && BM == 128 && BN == 128) {
-      // at least two full rounds of query blocks per XCD: three 4-wavefront
-      // workgroups per compute unit (packed and gathered sources alike, so the
-      // two forms of a call stay bit-identical)
-      const int64_t cux = cus_per_xcd();
-      if (cux > 0 && a.xcd_items >= 2 * cux) return launch_int8_cu3(a, grid, a.kv_tok != nullptr, s);
-      if (a.kv_tok != nullptr)
+  // D 128, 128 x 128 blocks: 3-slot rings.  With at least two full rounds of
+  // query blocks per XCD, three 4-wavefront workgroups per compute unit
+  // (32-key steps); otherwise one 8-wavefront workgroup (int8: 128-key steps
+  // of 48 KiB, bf16: 64-key steps of 32 KiB).  Packed and gathered sources of
+  // one shape take the same form, so the two forms of a call stay bit-identical.
+  if (D == 128 && BM == 128 && BN == 128) {
+    const int64_t cux = cus_per_xcd();
+    const bool cu3 = cux > 0 && a.xcd_items >= 2 * cux;
+    const bool bits = a.kmask != nullptr, gather = a.kv_tok != nullptr;
+    if constexpr (INT8) {
+      if (cu3) return launch_int8_cu3(a, grid, gather, bits, s);
+      if (gather)
         sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true, true><<<grid, dim3(512), 0, s>>>(a);
-      else
+      else if (bits)
         sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, true><<<grid, dim3(512), 0, s>>>(a);
-      return launch_status();
-    }
-  }
-  if constexpr (!INT8) {  // bf16 at D 128: a 3-slot ring of 64-key steps (3 x 32 KiB)
-    if (D == 128 && BM == 128 && BN == 128) {
-      // validity bits and at least two full rounds of query blocks per XCD:
-      // three 4-wavefront workgroups per compute unit, 32-key steps (3 x 16.25 KiB)
-      const int64_t cux = cus_per_xcd();
-      const bool cu3 = a.kmask != nullptr && cux > 0 && a.xcd_items >= 2 * cux;
-      if (a.kv_tok != nullptr)
-        return cu3 ? launch_bf16_gather_cu3(a, grid, s) : launch_bf16_gather(a, grid, s);
-      if (cu3)
+      else
+        sparse_attn_kernel<true, 128, 128, 128, 3, 128, 2, false><<<grid, dim3(512), 0, s>>>(a);
+    } else {
+      if (cu3 && bits && !gather)  // built here, for instruction-level parallelism
         sparse_attn_kernel<false, 128, 128, 128, 3, 32, 1, true, false, 3>
             <<<grid, dim3(256), 0, s>>>(a);
-      else if (a.kmask != nullptr)
+      else if (cu3)
+        return launch_bf16_cu3(a, grid, gather, s);
+      else if (gather)
+        return launch_bf16_gather(a, grid, s);
+      else if (bits)
         sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, true><<<grid, dim3(512), 0, s>>>(a);
       else
         sparse_attn_kernel<false, 128, 128, 128, 3, 64, 2, false><<<grid, dim3(512), 0, s>>>(a);
-      return launch_status();
     }
+    return launch_status();
   }
-  RCSA_ATTN(128, 128, 128, INT8 ? 3 : 2)
   RCSA_ATTN(128, 128, 64, 2)
   RCSA_ATTN(128, 64, 128, 2)
   RCSA_ATTN(128, 64, 64, 2)

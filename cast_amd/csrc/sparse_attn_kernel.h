@@ -966,12 +966,12 @@ attn_merge_kernel(AttnArgs a) {
 // the default instruction scheduler: the kernels of sparse_attn.hip are
 // scheduled for instruction-level parallelism, which makes this one slower.
 int launch_bf16_gather(AttnArgs& a, dim3 grid, hipStream_t s);
-// The same as three 4-wavefront workgroups per compute unit
-// (sparse_attn_bf16_gather_cu3.hip).
-int launch_bf16_gather_cu3(AttnArgs& a, dim3 grid, hipStream_t s);
-// The int8 kernel with validity bits as three 4-wavefront workgroups per
-// compute unit (sparse_attn_int8_cu3.hip); `gather` selects the V slot-map form.
-int launch_int8_cu3(AttnArgs& a, dim3 grid, bool gather, hipStream_t s);
+// Three 4-wavefront workgroups per compute unit (sparse_attn_int8_cu3.hip,
+// sparse_attn_bf16_cu3.hip): int8 with gathered V (bits) or packed sources
+// (bits or bytes); bf16 with gathered sources (bits) or packed ones with
+// validity bytes.
+int launch_int8_cu3(AttnArgs& a, dim3 grid, bool gather, bool bits, hipStream_t s);
+int launch_bf16_cu3(AttnArgs& a, dim3 grid, bool gather, hipStream_t s);
 
 }  // namespace rcsa
 
