@@ -49,9 +49,12 @@ def test_noalloc_matches_split_entry_point(dev):
     from cast_amd import _lib
     lib = _lib.load()
     assert lib.rcsa_attn_noalloc_scratch_bytes() == 32 << 20
-    # 12 heads x 28 query blocks: 42 items per XCD -> 32 whole + 10 tail items each;
-    # then 2 heads x 20 query blocks: 5 items per XCD, all tail items
-    for seed, H, nqb, nkb, max_k, n_split in ((1, 12, 28, 40, 24, 3), (2, 2, 20, 16, 10, 4)):
+    # 24 heads x 28 query blocks: 84 items per XCD, two full rounds (the kernel of three
+    # workgroups per compute unit) + 20 tail items each; then 12 heads x 28 query
+    # blocks: 42 items per XCD -> 32 whole + 10 tail items each; then 2 heads x 20
+    # query blocks: 5 items per XCD, all tail items (each call smaller than the last)
+    for seed, H, nqb, nkb, max_k, n_split in ((3, 24, 28, 40, 24, 3), (1, 12, 28, 40, 24, 3),
+                                              (2, 2, 20, 16, 10, 4)):
         print(f"noalloc H{H} nqb{nqb} nkb{nkb} max_k{max_k} n_split{n_split}", flush=True)
         args = _inputs(seed, H, nqb, nkb, max_k, dev)
         nbytes = int(lib.rcsa_attn_workspace_bytes(1, H, nqb * 128, 128, n_split))
