@@ -527,7 +527,9 @@ def main() -> int:
                 r.q_i8, r.q_scale, r.k_i8, r.k_scale, lw.v, r.indices, r.counts, None, out=o,
                 block_mask=r.k_mask), 10, 2)
             tops = ops_l / ms_l / 1e9
+            call_l = _events_time(lambda: layer_call(lw), 10, 2)
             per_layer.append({"query_frames": p["query_frames"], "fraction": p["fraction"],
+                              "layer_call_ms": round(call_l, 4),
                               "attn_ms": round(ms_l, 4), "attn_TOPS": round(tops, 1),
                               "frac_int8_peak": round(tops / INT8_PEAK_TOPS, 4),
                               "frac_mixed_ceiling": round(tops / MIXED_CEILING_TOPS, 4)})
