@@ -11,9 +11,11 @@ quantiser), pooled K (+ smoothing statistics), block scores, top-k
 selection, int8 K quantiser, block-sparse attention.  Inputs are resident in
 HBM before the timed region.  Every timed region follows 40-60 ms of the same
 work (the device's clock ramp after idle), then --warmup steps, then exactly
---steps timed steps.
+--steps timed steps.  By default each timed step is one replay of a HIP graph
+holding the layer call's launches (checked equal to the eager call); the
+eager call's time is reported beside it.
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--launch graph|eager]
 
 prints ONE JSON line.
 """
@@ -87,6 +89,26 @@ def _read_traffic():
     except OSError:
         pass
     return None
+
+
+def _capture(fn):
+    """(HIP graph of one ``fn()`` call, that call's result): three warm calls on a
+    side stream, then the capture (torch's graph memory pool keeps the captured
+    outputs; nothing in the layer call writes memory with a memset)."""
+    import torch
+    cur = torch.cuda.current_stream()
+    side = torch.cuda.Stream()
+    side.wait_stream(cur)
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            fn()
+    cur.wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        res = fn()
+    torch.cuda.synchronize()
+    return graph, res
 
 
 def cpu_baseline(seed: int, heads: int) -> dict:
@@ -267,6 +289,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-extras", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=24)
+    ap.add_argument("--launch", choices=["graph", "eager"], default="graph",
+                    help="issue each timed layer call as one HIP graph replay (default) "
+                         "or as the eager Python call")
     ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer", "compact",
                                        "compact_bf16", "router", "qkv"],
                     default=None,
@@ -346,16 +371,39 @@ def main() -> int:
 
     # one int8 attention dispatch per step: the timed ones are dispatches
     # [first_timed, first_timed + steps) of this process (a kernel trace's order)
-    first_timed = _prewarm(step, 60.0) + args.warmup
+    dispatched = _prewarm(step, 60.0) + args.warmup
     for _ in range(args.warmup):
         res = step()
-    # HIP events around the entry points of every timed step, on the stream
-    # they launch on (torch's current stream): the attention's launch time for
-    # the roofline, and the fused pooling and quantiser/selection launches as
-    # they run inside the layer call (K no longer in the MALL from the step before).
-    # Only the attention's pair of events sits in the timed steps (each recorded
-    # event adds GPU time between the launches); the pooling and quantiser /
-    # selection launches are timed the same way in as many steps right after.
+    run = step
+    if args.launch == "graph":
+        # The layer call captured once in a HIP graph and replayed: the same
+        # launches, arguments and buffers as the eager call, issued by one
+        # graph launch per step, so that the host's speed (a fresh box's
+        # Python thread can take 100-260 us per eager call) never leaves the
+        # GPU waiting between steps.  Every replay must equal the eager call.
+        graph, gres = _capture(step)
+        dispatched += 3
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            if not (torch.equal(gres.out, res.out) and torch.equal(gres.indices, res.indices)
+                    and torch.equal(gres.counts, res.counts)):
+                raise RuntimeError("bench.py: the graph replay differs from the eager layer call")
+            step()  # eager work between the replays
+        dispatched += 6
+        run = graph.replay
+        dispatched += _prewarm(run, 60.0) + args.warmup
+        for _ in range(args.warmup):
+            run()
+        res = gres
+    first_timed = dispatched
+    # HIP events around the entry points of the layer call, on the stream they
+    # launch on (torch's current stream): the attention's launch time for the
+    # roofline, and the fused pooling and quantiser/selection launches as they
+    # run inside the layer call (K no longer in the MALL from the step before).
+    # No event sits in the timed steps (each recorded event adds GPU time
+    # between the launches, about 24 us per step for one pair); the entry points
+    # are timed this way in as many steps right after them.
     names = ("sparse_attn_int8", "pool_query_key", "quantize_key_select")
     events = {n: [] for n in names}
     entries = {n: getattr(ops, n) for n in names}
@@ -386,13 +434,20 @@ def main() -> int:
 
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    res = instrumented(names[:1], args.steps)
+    for _ in range(args.steps):
+        run()
     t_enqueued = time.perf_counter()  # the host has issued every timed step
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / args.steps
     host_ms_per_step = (t_enqueued - t0) * 1e3 / args.steps
-    instrumented(names[1:], args.steps)
+    instrumented(names, args.steps)
     torch.cuda.synchronize()
+    # the same steps issued by the eager Python call, for comparison
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    eager_ms_per_step = (time.perf_counter() - t1) * 1e3 / args.steps
     call_ms = {n: statistics.fmean(a.elapsed_time(b) for a, b in ev) for n, ev in events.items()}
     attn_ms = call_ms["sparse_attn_int8"]
     ops_attn = w.attention_ops(res.indices, res.counts)
@@ -468,7 +523,8 @@ def main() -> int:
     ns_plan = ctypes.c_int64(0)
     _lib.load().rcsa_attn_split_plan(B, H, Lq, bs, max_k, ctypes.byref(ns_plan))
     extras = {"stage_ms": stage_ms, "layer_call_ms": call_ms, "hbm": hbm_frac,
-              "host_enqueue_ms_per_step": host_ms_per_step,
+              "launch": args.launch, "host_enqueue_ms_per_step": host_ms_per_step,
+              "eager_ms_per_step": eager_ms_per_step,
               "ms_per_layer_call": ms_per_step,
               "attn_split_plan": ns_plan.value,
               "attn_timed_dispatches": [first_timed, args.steps]}
