@@ -32,22 +32,35 @@ docstring; the pins live in tests/test_oracle_pins.py:
   closed_loop_degrees conserved edge budgets (every worldline Tc * mean, the
                       whole layer blocks * mean); uniform curvature gives
                       uniform degrees; a pure-Python Fraction re-derivation
-                      on small cases
+                      on small cases; equal to the reference's own
+                      compact_closed_loop_degrees on fixtures it wrote (all
+                      three feedback forms with a response, bootstrap, weight
+                      0, fixed budget, prefix frames, partial cells, a row
+                      over capacity: tests/golden/ref_closed_loop.npz)
   omission_proxy      fp64 loops over rows, candidates and sketch groups
   route_objective_terms / route_objective_value
                       the quadratic terms reproduce the brute-force change of
                       the objective value for every single-row change (with the
-                      identity operator and with random operators)
+                      identity operator and with random operators); equal to the
+                      reference's _objective_value / _objective_terms with no
+                      transport and with a published one
+                      (tests/golden/ref_router.npz)
   transport_maps      exponent 0 and theta 0 give no change; the windows are cut
                       and overlap-added with explicit index loops (a different
-                      formulation from the product's unfold/fold)
+                      formulation from the product's unfold/fold); equal to the
+                      reference's _apply_transport_maps and _transport_matrix
+                      on pooled and unpooled transport grids, exponents of both
+                      signs (tests/golden/ref_router.npz)
   quantize_rows_int8  error <= scale / 2, the absmax element maps to +-127, zero rows
   int8_linear         pure-Python integer dot products on small shapes; exact
                       int32 accumulation bound; scales factor out
   fc_pasm_refine      the identity (with the reference's fallback reasons) for
                       every missing-transport / disabled case; the chosen swap
                       equals a brute-force search over every admissible
-                      single swap of the objective value
+                      single swap of the objective value; the same routes,
+                      swap counts and objectives as the reference's refine
+                      with a published transport (same bank on and off, one
+                      and two rounds: tests/golden/ref_router.npz)
 """
 from __future__ import annotations
 

@@ -1,0 +1,291 @@
+"""Write reference-produced fixtures for the router transport / objective /
+refine and the closed-loop allocator: ``tests/golden/ref_router.npz`` and
+``tests/golden/ref_closed_loop.npz``.
+
+Run in the build container only (the reference never travels to a GPU box):
+
+    python tests/golden/make_ref_golden.py [/path/to/CAST]
+
+It imports two torch-only modules of the CAST reference and records, on small
+seeded CPU inputs, what these functions return:
+
+* ``FCPASMLocalCoordinateSwapRouter._apply_transport_maps`` and
+  ``._transport_matrix`` (P/fc_pasm_swap_routing.py:116-412): a pooled
+  transport grid (11 x 10 windows averaged to 6 x 5) and an unpooled one
+  (8 x 8 windows), exponents of both signs;
+* ``._objective_value`` and ``._objective_terms`` (:414-614), with no
+  transport (g = 0) and with a published transport;
+* ``.refine`` (:616-1077), four calls with a published transport: same-bank
+  on and off, one and two rounds;
+* ``MatrixControlResponseCWCAAttentionCompiler._compact_time_cells``,
+  ``._redistribute_compact_capacity`` and ``.compact_closed_loop_degrees``
+  (P/control_response_cwca_attention.py:1123-1363): the additive, centred
+  multiplicative and centred inverse feedback forms with a nonzero response,
+  the layer-0 bootstrap, response weight 0, the fixed query budget, prefix
+  frames before the profiled offset, a partial last cell and a peaked
+  curvature that saturates rows.  The method runs on an instance whose
+  attributes are set directly (the fields it reads), not through compile().
+
+Fixtures hold inputs and outputs only (numpy arrays, no pickles); the tests
+feed the inputs to the oracle and the product and compare with the outputs.
+P/ = src/interaction_accel/methods/proposed/.
+"""
+from __future__ import annotations
+
+import math
+import os
+import sys
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+REF = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+sys.path.insert(0, os.path.join(REF, "src"))
+
+from interaction_accel.methods.proposed import fc_pasm_swap_routing as R  # noqa: E402
+from interaction_accel.methods.proposed import control_response_cwca_attention as C  # noqa: E402
+
+Router = R.FCPASMLocalCoordinateSwapRouter
+
+# transport geometries: (output, transport, window, stride, padding, tile grid, block grid)
+GEOMETRIES = {
+    "pooled": ((22, 40), (6, 5), (11, 10), (8, 8), (4, 5), (3, 6), (6, 5)),
+    "unpooled": ((16, 20), (8, 8), (8, 8), (4, 4), (2, 2), (4, 5), (4, 5)),
+}
+
+
+def transport_dict(name, seed, pairs, mean_affinity=0.9):
+    out, tr, win, stride, pad, grid, _ = GEOMETRIES[name]
+    g = torch.Generator().manual_seed(seed)
+    tiles = grid[0] * grid[1]
+    spec = (tr[0], tr[1] // 2 + 1)
+    entries = {}
+    for p in pairs:
+        entries[p] = {"theta": (torch.rand(tiles, *spec, generator=g) * 2 - 1) * math.pi,
+                      "affinity": torch.rand(tiles, *spec, generator=g),
+                      "mean_affinity": torch.tensor(mean_affinity)}
+    return {"output_shape": out, "transport_shape": tr, "window_shape": win, "stride": stride,
+            "padding": pad, "tile_grid": grid, "pairs": entries}
+
+
+def put_transport(fx, prefix, name, tr):
+    out, trs, win, stride, pad, grid, block = GEOMETRIES[name]
+    fx[f"{prefix}geometry"] = np.array([*out, *trs, *win, *stride, *pad, *grid, *block],
+                                       dtype=np.int64)
+    pairs = sorted(tr["pairs"])
+    fx[f"{prefix}pairs"] = np.array(pairs, dtype=np.int64).reshape(-1, 2)
+    for i, p in enumerate(pairs):
+        e = tr["pairs"][p]
+        fx[f"{prefix}theta{i}"] = e["theta"].numpy()
+        fx[f"{prefix}affinity{i}"] = e["affinity"].numpy()
+        fx[f"{prefix}mean_affinity{i}"] = np.float32(float(e["mean_affinity"]))
+
+
+def transport_cases(fx):
+    for ci, (name, exps) in enumerate((("pooled", (0.25, -0.6, 1.0)),
+                                       ("unpooled", (0.4, -0.35, -1.0)))):
+        block = GEOMETRIES[name][6]
+        tr = transport_dict(name, 100 + ci, [(0, 6)])
+        put_transport(fx, f"transport{ci}_", name, tr)
+        g = torch.Generator().manual_seed(200 + ci)
+        maps = torch.randn(3, 2, *block, generator=g)
+        fx[f"transport{ci}_maps"] = maps.numpy()
+        fx[f"transport{ci}_exponents"] = np.array(exps, dtype=np.float32)
+        for j, a in enumerate(exps):
+            moved, used = Router._apply_transport_maps(tr, (0, 6), maps, spatial_shape=block,
+                                                       exponent=a)
+            assert used
+            fx[f"transport{ci}_maps_out{j}"] = moved.numpy()
+            mat, used = Router._transport_matrix(tr, (0, 6), spatial_shape=block,
+                                                 device=torch.device("cpu"), exponent=a)
+            assert used
+            fx[f"transport{ci}_matrix{j}"] = mat.numpy()
+
+
+OBJ_KW = dict(temporal_cells=3, exact_frames=(0, 3, 7, 9), temporal_group_size=4,
+              current_boundary=8, lambda_anchor=1.0, lambda_reconstruction=0.7)
+
+
+def objective_cases(fx):
+    name = "pooled"
+    block = GEOMETRIES[name][6]
+    S = block[0] * block[1]
+    tr = transport_dict(name, 300, [(0, 3), (3, 7)])
+    tr = dict(tr, attention_spatial_h=block[0], attention_spatial_w=block[1])
+    put_transport(fx, "objective_", name, tr)
+    g = torch.Generator().manual_seed(301)
+    err = torch.randn(1, 2, OBJ_KW["temporal_cells"] * S, 4, generator=g) * 0.1
+    fx["objective_error"] = err.numpy()
+    fx["objective_frames"] = np.array(OBJ_KW["exact_frames"], dtype=np.int64)
+    fx["objective_params"] = np.array([OBJ_KW["temporal_cells"], OBJ_KW["temporal_group_size"],
+                                       OBJ_KW["current_boundary"]], dtype=np.int64)
+    fx["objective_lambdas"] = np.array([OBJ_KW["lambda_anchor"],
+                                        OBJ_KW["lambda_reconstruction"]], dtype=np.float32)
+    for tag, t in (("g0", None), ("fc", tr)):
+        v = Router._objective_value(err, spatial=S, transport=t, **OBJ_KW)
+        a, b, _, used, terms = Router._objective_terms(err, spatial=S, transport=t, **OBJ_KW)
+        assert used == (t is not None) and terms == 5
+        fx[f"objective_{tag}_value"] = np.float32(float(v))
+        fx[f"objective_{tag}_a"] = a.numpy()
+        fx[f"objective_{tag}_b"] = b.numpy()
+
+
+# refine: a compact layer of 63 memory blocks and 4 current cells of 6 x 5
+MEM, CELLS, D, HEADS, K = 63, 4, 64, 2, 24
+
+
+def local_stencil(n, nh, nw):
+    ids = torch.arange(n)
+    spatial = nh * nw
+    bt, rem = ids // spatial, ids % spatial
+    bh, bw = rem // nw, rem % nw
+    return ((bt[:, None] - bt[None, :]).abs() + (bh[:, None] - bh[None, :]).abs()
+            + (bw[:, None] - bw[None, :]).abs()) <= 1
+
+
+def refine_cases(fx):
+    block = GEOMETRIES["pooled"][6]
+    S = block[0] * block[1]
+    N = MEM + CELLS * S
+    local = local_stencil(N, *block)
+    cases = [(True, 1), (False, 1), (True, 2), (False, 2)]
+    fx["refine_cases"] = np.array(cases, dtype=np.int64)
+    fx["refine_params"] = np.array([MEM, CELLS, block[0], block[1], 4, 8, 22], dtype=np.int64)
+    fx["refine_frames"] = np.array([0, 6], dtype=np.int64)
+    for ci, (same_bank, rounds) in enumerate(cases):
+        g = torch.Generator().manual_seed(400 + ci)
+        qh = torch.nn.functional.normalize(torch.randn(1, HEADS, N, D, generator=g), dim=-1)
+        kh = torch.nn.functional.normalize(torch.randn(1, HEADS, N, D, generator=g) + qh * 0.3,
+                                           dim=-1)
+        score = qh @ kh.transpose(-1, -2)
+        pooled_v = torch.randn(1, HEADS, N, D, generator=g) * 0.5
+        rank = score + local[None, None] * 1e6
+        sel = torch.sort(rank, dim=-1, descending=True, stable=True).indices[..., :K]
+        counts = torch.randint(K - 6, K + 1, (1, HEADS, N), generator=g)
+        tr = transport_dict("pooled", 410 + ci, [(0, 6)])
+        put_transport(fx, f"refine{ci}_", "pooled", tr)
+        tr = dict(tr, attention_spatial_h=block[0], attention_spatial_w=block[1])
+        cfg = R.FCPASMSwapRoutingConfig(candidate_multiplier=2, num_swap_rounds=rounds,
+                                        swap_eps=1e-6, sketch_groups=16,
+                                        require_fc_transport=True, min_transport_affinity=0.5,
+                                        same_bank_only=same_bank)
+        # refine writes its swaps into the route it is given (the scatter into
+        # selected[..., memory:, :] at :950-960), so it gets a copy
+        out, rec = Router(cfg).refine(score=score, pooled_value=pooled_v, selected=sel.clone(),
+                                      counts=counts, local=local, memory_blocks=MEM,
+                                      spatial_shape=block, exact_current_frames=(0, 6),
+                                      temporal_group_size=4, current_boundary=8, transport=tr,
+                                      layer_index=22)
+        assert rec["status"] == "refined" and rec["swap_count"] >= 1, rec
+        for key, val in (("score", score), ("pooled_value", pooled_v), ("selected", sel),
+                         ("counts", counts), ("out", out)):
+            fx[f"refine{ci}_{key}"] = val.numpy()
+        fx[f"refine{ci}_swap_count"] = np.int64(rec["swap_count"])
+        fx[f"refine{ci}_objective"] = np.array([float(rec["objective_before"]),
+                                                float(rec["objective_after"])])
+        fx[f"refine{ci}_historical_budget"] = np.array(
+            [int(rec["historical_budget_before"]), int(rec["historical_budget_after"])])
+
+
+# closed loop: CWCA source tiles of 4 frames, 6 spatial worldlines
+def provider(curvature, *, offset, block_t, feedback, weight, fixed, layer, responses):
+    p = object.__new__(C.MatrixClosedLoopCWCAAttentionCompiler)
+    p.mode = "closed_loop"
+    p._compact_layer_index = layer
+    p._layer_index = layer
+    p._curvature_matrix = curvature
+    p._current_temporal_offset = offset
+    p._block_shape = (block_t, 1, 1)
+    p.fixed_query_budget = fixed
+    p.response_weight = weight
+    p.feedback_form = feedback
+    p._responses = responses
+    p._call_index = 0
+    return p
+
+
+CL_CASES = [
+    # (feedback, weight, layer, fixed, offset, frames (current-local), compact group,
+    #  mean, memory rows, peaked); total rows = memory + cells * 6
+    ("additive", 0.5, 3, False, 3, list(range(0, 16)), 4, 61, 183, False),
+    ("centered_multiplicative", 0.7, 5, False, 3, list(range(0, 16)), 4, 61, 183, False),
+    ("centered_inverse", 0.7, 5, False, 3, list(range(0, 16)), 4, 61, 183, False),
+    ("additive", 0.5, 0, False, 3, list(range(0, 16)), 4, 61, 183, False),
+    ("additive", 0.0, 4, False, 3, list(range(0, 16)), 4, 61, 183, False),
+    ("additive", 0.5, 4, True, 3, list(range(0, 16)), 4, 61, 183, False),
+    ("centered_inverse", 1.3, 2, False, 1, [0, 2, 5, 6, 7, 9, 12], 3, 40, 24, False),
+    ("additive", 0.8, 7, False, 0, [1, 2, 3, 4, 5, 6, 7, 8, 9, 10], 2, 31, 2, True),
+]
+
+
+def closed_loop_cases(fx):
+    S = 6
+    fx["cl_count"] = np.int64(len(CL_CASES))
+    for ci, (form, weight, layer, fixed, offset, frames, cg, mean, memory,
+             peaked) in enumerate(CL_CASES):
+        g = torch.Generator().manual_seed(500 + ci)
+        t_src = 4
+        curvature = torch.rand(t_src, S, generator=g) + 0.05
+        if peaked:
+            curvature[1, 2] = 60.0
+        response = torch.rand(t_src, S, generator=g) * 2
+        cells = math.ceil(len(frames) / cg)
+        total = memory + cells * S
+        base = max(7, math.ceil(4 * mean / 5))
+        p = provider(curvature, offset=offset, block_t=4, feedback=form, weight=weight,
+                     fixed=fixed, layer=layer, responses={layer - 1: response})
+        origin = 40
+        active = torch.tensor(frames, dtype=torch.long) + origin
+        deg, meta = p.compact_closed_loop_degrees(
+            layer_index=layer, active_current=active, current_frame_origin=origin,
+            temporal_group_size=cg, spatial_blocks=S, mean_degree=mean, base_degree=base,
+            total_blocks=total, memory_blocks=memory)
+        assert deg.shape == (cells, S) and cells * S == total - memory, (ci, deg.shape)
+        pre = f"cl{ci}_"
+        fx[pre + "curvature"] = curvature.numpy()
+        fx[pre + "response"] = response.numpy()
+        fx[pre + "frames"] = np.array(frames, dtype=np.int64)
+        fx[pre + "params"] = np.array([layer, int(fixed), offset, 4, cg, mean, base, total,
+                                       memory], dtype=np.int64)
+        fx[pre + "form"] = np.array(form)
+        fx[pre + "weight"] = np.float32(weight)
+        fx[pre + "degrees"] = deg.numpy()
+        fx[pre + "source"] = np.array(meta["source"])
+        fx[pre + "budgets"] = np.array([meta["current_worldline_budget"],
+                                        meta["current_edge_budget"], meta["global_edge_budget"],
+                                        meta["reference_edge_budget"]], dtype=np.int64)
+        cs = meta["curvature"]
+        fx[pre + "curvature_stats"] = np.array([cs["min"], cs["max"], cs["mean"], cs["std"]],
+                                               dtype=np.float64)
+        # the helpers on their own
+        normalized = curvature / curvature.mean(dim=0, keepdim=True).clamp_min(
+            torch.finfo(curvature.dtype).eps)
+        cells_t = C.MatrixControlResponseCWCAAttentionCompiler._compact_time_cells(
+            normalized, torch.tensor(frames), cg, 4, offset)
+        fx[pre + "time_cells"] = cells_t.numpy()
+    # redistribution alone: a column over capacity, a column exactly at it
+    deg = torch.tensor([[12, 3, 9], [2, 4, 9], [0, 11, 9]], dtype=torch.long)
+    fx["redistribute_in"] = deg.numpy()
+    fx["redistribute_out"] = C.MatrixControlResponseCWCAAttentionCompiler \
+        ._redistribute_compact_capacity(deg.clone(), capacity=10,
+                                        target_per_worldline=18).numpy()
+
+
+def main():
+    torch.manual_seed(0)
+    fx = {}
+    transport_cases(fx)
+    objective_cases(fx)
+    refine_cases(fx)
+    np.savez_compressed(os.path.join(HERE, "ref_router.npz"), **fx)
+    fc = {}
+    closed_loop_cases(fc)
+    np.savez_compressed(os.path.join(HERE, "ref_closed_loop.npz"), **fc)
+    for name, d in (("ref_router.npz", fx), ("ref_closed_loop.npz", fc)):
+        size = os.path.getsize(os.path.join(HERE, name))
+        print(f"wrote {name}: {len(d)} arrays, {size / 1024:.0f} KiB")
+
+
+if __name__ == "__main__":
+    main()

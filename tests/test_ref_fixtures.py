@@ -1,0 +1,139 @@
+"""The oracle's router transport / objective / refine and closed-loop allocator
+against fixtures the CAST reference itself produced (tests/golden/make_ref_golden.py:
+P/fc_pasm_swap_routing.py:116-1077, P/control_response_cwca_attention.py:1123-1363),
+and the product's host-side transport operator against the same fixtures.
+
+The GPU router and allocator are compared with these fixtures in
+tests/test_gpu_ref_fixtures.py.
+"""
+import numpy as np
+import pytest
+import torch
+
+from tests._ref_fixtures import (closed_loop_case, closed_loop_count, objective_case,
+                                 oracle_operator, refine_case, refine_count, router_fixture,
+                                 transport_case)
+from oracle import rcsa_oracle as orc
+
+
+@pytest.mark.parametrize("ci", [0, 1])
+def test_oracle_transport_maps_match_reference(ci):
+    tr, block, maps, exps, outs, mats = transport_case(ci)
+    S = block[0] * block[1]
+    eye = torch.eye(S).reshape(S, 1, *block)
+    for a, want, want_mat in zip(exps, outs, mats):
+        got = maps + orc.transport_maps(tr, (0, 6), maps, float(a))
+        torch.testing.assert_close(got, want, atol=2e-6, rtol=1e-5)
+        # the operator [output, input]: transport of the unit maps, transposed
+        op = (torch.eye(S) + orc.transport_maps(tr, (0, 6), eye, float(a)).reshape(S, S)).T
+        torch.testing.assert_close(op, want_mat, atol=2e-6, rtol=1e-5)
+
+
+@pytest.mark.parametrize("ci", [0, 1])
+def test_product_transport_operator_matches_reference(ci):
+    from cast_amd.transport import fc_transport_operator, transport_maps
+    tr, block, maps, exps, outs, mats = transport_case(ci)
+    for a, want, want_mat in zip(exps, outs, mats):
+        op = fc_transport_operator(tr, (0, 6), block, float(a))
+        torch.testing.assert_close(op, want_mat, atol=2e-6, rtol=1e-5)
+        torch.testing.assert_close(maps + transport_maps(tr, (0, 6), maps, float(a)), want,
+                                   atol=2e-6, rtol=1e-5)
+
+
+def test_transport_fixture_is_not_trivial():
+    """The fixture would catch a transposed operator or a conjugated phase: the
+    reference's operators are far from symmetric and from the zero-phase identity,
+    and exponents of opposite sign give different operators."""
+    for ci in (0, 1):
+        tr, block, maps, exps, outs, mats = transport_case(ci)
+        S = block[0] * block[1]
+        for m in mats:
+            assert float((m - torch.eye(S)).abs().max()) > 1e-2
+            assert float((m - m.T).abs().max()) > 1e-3
+        assert float((mats[0] - mats[1]).abs().max()) > 1e-2
+
+
+@pytest.mark.parametrize("tag", ["g0", "fc"])
+def test_oracle_objective_matches_reference(tag):
+    err, kw, op, want_value, want_a, want_b = objective_case(tag)
+    value = orc.route_objective_value(err, operator=op, **kw)
+    a, b, used = orc.route_objective_terms(err, operator=op, **kw)
+    assert used == (tag == "fc")
+    assert abs(float(value) - want_value) <= 1e-5 * abs(want_value)
+    torch.testing.assert_close(a, want_a, atol=1e-5, rtol=1e-5)
+    torch.testing.assert_close(b, want_b, atol=1e-6, rtol=1e-4)
+
+
+def test_objective_fixture_distinguishes_transport():
+    _, _, _, v0, a0, b0 = objective_case("g0")
+    _, _, _, v1, a1, b1 = objective_case("fc")
+    assert abs(v0 - v1) > 1e-3 * abs(v0)
+    assert float((a0 - a1).abs().max()) > 1e-3
+
+
+@pytest.mark.parametrize("ci", range(refine_count()))
+def test_oracle_refine_matches_reference(ci):
+    c = refine_case(ci)
+    want_out, _, _ = c["out"], c["swap_count"], c["objective"]
+    got, rec = orc.fc_pasm_refine(c["score"], c["pooled_value"], c["selected"], c["counts"],
+                                  c["local"], transport=c["transport"], config=c["config"],
+                                  operator=oracle_operator(c["transport"], c["block"]),
+                                  **c["kw"])
+    assert rec["status"] == "refined"
+    assert rec["swap_count"] == c["swap_count"]
+    assert torch.equal(got, want_out)
+    before, after = c["objective"]
+    assert abs(rec["objective_before"] - before) <= 1e-5 * abs(before)
+    assert abs(rec["objective_after"] - after) <= 1e-5 * abs(after)
+    assert [rec["historical_budget_before"], rec["historical_budget_after"]] == \
+        list(c["historical_budget"])
+
+
+def test_refine_fixtures_change_the_route():
+    for ci in range(refine_count()):
+        c = refine_case(ci)
+        assert not torch.equal(c["out"], c["selected"])
+        assert c["objective"][1] < c["objective"][0]
+
+
+@pytest.mark.parametrize("ci", range(closed_loop_count()))
+def test_oracle_closed_loop_matches_reference(ci):
+    c = closed_loop_case(ci)
+    p = c["params"]
+    got = orc.closed_loop_degrees(c["curvature"], c["frames"], **c["oracle_kw"])
+    mem = p["memory"]
+    assert torch.equal(got[:mem], torch.full((mem,), p["mean"], dtype=torch.long))
+    assert torch.equal(got[mem:], c["degrees"].reshape(-1))
+    cells = orc.compact_time_cells(c["normalized"], c["frames"], p["compact_group"], 4,
+                                   p["offset"])
+    torch.testing.assert_close(cells, c["time_cells"], atol=0, rtol=0)
+
+
+def test_closed_loop_fixtures_cover_the_feedback_forms():
+    """The three feedback forms give three different allocations of the same
+    curvature and response, and the peaked case saturates a row at the layer's
+    block count."""
+    deg = [closed_loop_case(i)["degrees"] for i in range(3)]
+    assert not torch.equal(deg[0], deg[1]) and not torch.equal(deg[1], deg[2]) \
+        and not torch.equal(deg[0], deg[2])
+    peaked = closed_loop_case(closed_loop_count() - 1)
+    assert int(peaked["degrees"].max()) == peaked["params"]["total"]
+
+
+def test_oracle_redistribution_matches_reference():
+    fx = router_fixture("closed_loop")
+    got = orc.redistribute_compact_capacity(torch.from_numpy(fx["redistribute_in"]).clone(),
+                                            capacity=10, target_per_worldline=18)
+    assert torch.equal(got, torch.from_numpy(fx["redistribute_out"]))
+
+
+def test_planted_closed_loop_mistake_is_caught():
+    """A slip in the oracle (the centred inverse form with the sign of the
+    multiplicative one) no longer matches the reference's allocation."""
+    c = closed_loop_case(2)
+    kw = dict(c["oracle_kw"], feedback_form="centered_multiplicative")
+    got = orc.closed_loop_degrees(c["curvature"], c["frames"], **kw)
+    assert not torch.equal(got[c["params"]["memory"]:], c["degrees"].reshape(-1))
+    np.testing.assert_array_equal(
+        orc.closed_loop_degrees(c["curvature"], c["frames"], **c["oracle_kw"])
+        [c["params"]["memory"]:].numpy(), c["degrees"].reshape(-1).numpy())
