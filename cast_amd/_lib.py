@@ -58,6 +58,9 @@ SIGNATURES: dict[str, list] = {
                          _P, _P],
     "rcsa_route_best_swap": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I,
                              c_int, _P, _P, _P],
+    "rcsa_route_apply_swap": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                              c_float, _P],
+    "rcsa_route_check": [_P, _P, _P, _P, _I, _I, _I, _I, _P, _P],
     "rcsa_quantize_rows_int8": [_P, c_int, _I, _I, _I, _P, _P, _P],
     "rcsa_int8_linear": [_P, _P, _P, _P, _P, _I, _I, _I, _P, _I, _P],
     "rcsa_pack_tokens": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _P, _I, _P, _P],

@@ -26,6 +26,11 @@ __device__ __forceinline__ uint64_t rank_key(float r, int i) {
   return (static_cast<uint64_t>(0xffffffffu - u) << 32) | static_cast<uint32_t>(i);
 }
 
+__device__ __forceinline__ int wave_sum_i(int v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
 __device__ float route_block_sum(float v, float* red) {
   v = wave_sum(v);
   const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
@@ -223,12 +228,13 @@ struct SwapArgs {
 
 __global__ void __launch_bounds__(kRouteThreads)
 route_swap_kernel(SwapArgs a) {
-  extern __shared__ float s_rem[];                                // removable slots' proxies
+  extern __shared__ __attribute__((aligned(16))) float s_rem[];  // removable slots' proxies
   __shared__ int s_slot[kRouteMaxBlocks];                         // their slot numbers
   __shared__ uint8_t s_rmem[kRouteMaxBlocks];                     // removed block in memory
   __shared__ int s_pos[kRouteMaxBlocks];                          // candidate position of a block
   __shared__ uint8_t s_kept[kRouteMaxBlocks];
   __shared__ int s_nrem;
+  __shared__ float s_rterm[kRouteMaxBlocks];                      // removable slots' own terms
   __shared__ float s_bv[kRouteThreads / kWave];
   __shared__ int s_bf[kRouteThreads / kWave];
   const int N = a.n_blocks, rows = N - a.memory_blocks, M = a.memory_blocks;
@@ -273,14 +279,32 @@ route_swap_kernel(SwapArgs a) {
     s_rem[e] = pos >= 0 ? proxy[static_cast<int64_t>(pos) * G + g] : 0.0f;
   }
   __syncthreads();
+  // The quadratic form of an exchange (removed proxies r, added proxies c,
+  // d = r - c) expands as
+  //   sum_g ca (2 e_g d_g + d_g^2) + 2 lin_g d_g
+  //     = [ca |r|^2 + 2 r.w] + [ca |c|^2 - 2 c.w] - 2 ca (r.c),  w = ca e + lin,
+  // so each removable slot and each candidate get one term of their own and a
+  // pair costs one dot product over the groups.
   const float ca = a.coef[rr];
-  float err[kRouteMaxGroups], lin[kRouteMaxGroups];
+  float w[kRouteMaxGroups];
 #pragma unroll
-  for (int g = 0; g < kRouteMaxGroups; ++g) {
-    err[g] = g < G ? a.error[out_row * G + g] : 0.0f;
-    lin[g] = g < G ? a.linear[out_row * G + g] : 0.0f;
+  for (int g = 0; g < kRouteMaxGroups; ++g)
+    w[g] = g < G ? ca * a.error[out_row * G + g] + a.linear[out_row * G + g] : 0.0f;
+  for (int i = t; i < nrem; i += kRouteThreads) {
+    float r2 = 0.0f, rw = 0.0f;
+#pragma unroll
+    for (int g = 0; g < kRouteMaxGroups; ++g) {
+      if (g < G) {
+        const float r = s_rem[i * G + g];
+        r2 = fmaf(r, r, r2);
+        rw = fmaf(r, w[g], rw);
+      }
+    }
+    s_rterm[i] = ca * r2 + 2.0f * rw;
   }
+  __syncthreads();
   const int limit = min(a.cand_mult * cnt, N);
+  const float m2ca = -2.0f * ca;
   float bv = INFINITY;
   int bf = 0x7fffffff;
   if (gated) {
@@ -288,21 +312,35 @@ route_swap_kernel(SwapArgs a) {
       const int c = cand[l];
       if (l >= limit || s_kept[c]) continue;  // not addable
       float add[kRouteMaxGroups];
+      float c2 = 0.0f, cw = 0.0f;
 #pragma unroll
-      for (int g = 0; g < kRouteMaxGroups; ++g)
+      for (int g = 0; g < kRouteMaxGroups; ++g) {
         add[g] = g < G ? proxy[static_cast<int64_t>(l) * G + g] : 0.0f;
+        c2 = fmaf(add[g], add[g], c2);
+        cw = fmaf(add[g], w[g], cw);
+      }
+      const float aterm = ca * c2 - 2.0f * cw;
       const uint8_t add_mem = c < M;
       // every lane reads the same removable slot at a time (LDS broadcasts)
       for (int i = 0; i < nrem; ++i) {
         if (a.same_bank && s_rmem[i] != add_mem) continue;
-        float imp = 0.0f;
+        float dot = 0.0f;
+        if (G == kRouteMaxGroups) {
+          const float4* r4 = reinterpret_cast<const float4*>(s_rem + i * kRouteMaxGroups);
 #pragma unroll
-        for (int g = 0; g < kRouteMaxGroups; ++g) {
-          if (g < G) {
-            const float dl = s_rem[i * G + g] - add[g];
-            imp += ca * (2.0f * err[g] * dl + dl * dl) + 2.0f * lin[g] * dl;
+          for (int q = 0; q < kRouteMaxGroups / 4; ++q) {
+            const float4 r = r4[q];
+            dot = fmaf(r.x, add[4 * q], dot);
+            dot = fmaf(r.y, add[4 * q + 1], dot);
+            dot = fmaf(r.z, add[4 * q + 2], dot);
+            dot = fmaf(r.w, add[4 * q + 3], dot);
           }
+        } else {
+#pragma unroll
+          for (int g = 0; g < kRouteMaxGroups; ++g)
+            if (g < G) dot = fmaf(s_rem[i * G + g], add[g], dot);
         }
+        const float imp = fmaf(m2ca, dot, s_rterm[i] + aterm);
         const int flat = s_slot[i] * L + l;
         if (imp < bv || (imp == bv && flat < bf)) {
           bv = imp;
@@ -334,6 +372,202 @@ route_swap_kernel(SwapArgs a) {
       }
     a.best[out_row] = bv;
     a.best_flat[out_row] = bv == INFINITY ? -1 : bf;
+  }
+}
+
+// One swap round's decision and its application, on the device
+// (P/fc_pasm_swap_routing.py:935-977): the strongest row is the first minimum
+// of best over all (bh, current row) (torch.argmin's order); when the swap limit
+// is not reached and its value is below -eps, its exchange replaces the kept
+// slot with the candidate and moves the row's error by the removed block's
+// proxy (zero when it is not a candidate of the row) minus the added one's.
+// Otherwise the refinement stops: later rounds change nothing.
+// state (int32): [0] swaps applied, [1] stopped, then per applied swap
+// [bh, row, slot, removed block, added block, improvement as float bits].
+struct ApplyArgs {
+  const float* best;          // [n_bh * rows]
+  const int32_t* best_flat;   // [n_bh * rows]
+  const int32_t* cand;        // [n_bh, rows, n_cand]
+  const float* proxy;         // [n_bh, rows, n_cand, groups]
+  int32_t* selected;          // [n_bh, n_blocks, max_k]
+  float* error;               // [n_bh, rows, groups]
+  int32_t* state;
+  int n_bh, n_blocks, memory_blocks, max_k, n_cand, groups, max_swaps, max_records;
+  float eps;
+};
+
+__global__ void __launch_bounds__(kRouteThreads)
+route_apply_kernel(ApplyArgs a) {
+  __shared__ float s_bv[kRouteThreads / kWave];
+  __shared__ int s_bi[kRouteThreads / kWave];
+  __shared__ int s_hit;
+  const int t = threadIdx.x;
+  const int rows = a.n_blocks - a.memory_blocks;
+  const int n = a.n_bh * rows;
+  const int swaps = a.state[0];
+  if (a.state[1] != 0) return;  // an earlier round stopped (uniform)
+  if ((a.max_swaps > 0 && swaps >= a.max_swaps) || swaps >= a.max_records) {
+    if (t == 0) a.state[1] = 1;
+    return;
+  }
+  float bv = INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = t; i < n; i += kRouteThreads) {
+    const float v = a.best[i];
+    if (v < bv || (v == bv && i < bi)) { bv = v; bi = i; }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(bv, o, kWave);
+    const int oi = __shfl_xor(bi, o, kWave);
+    if (ov < bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+  }
+  const int lane = t % kWave, wave = t / kWave;
+  if (lane == 0) { s_bv[wave] = bv; s_bi[wave] = bi; }
+  if (t == 0) s_hit = 0x7fffffff;
+  __syncthreads();
+  for (int w = 0; w < kRouteThreads / kWave; ++w)
+    if (s_bv[w] < bv || (s_bv[w] == bv && s_bi[w] < bi)) { bv = s_bv[w]; bi = s_bi[w]; }
+  // every thread now holds the same (bv, bi); rows with no exchange hold +inf
+  if (!(bv < -a.eps) || bi >= n) {
+    if (t == 0) a.state[1] = 1;
+    return;
+  }
+  const int fl = a.best_flat[bi];
+  if (fl < 0) {
+    if (t == 0) a.state[1] = 1;
+    return;
+  }
+  const int bh = bi / rows, rr = bi % rows, row = a.memory_blocks + rr;
+  const int slot = fl / a.n_cand, pos = fl % a.n_cand;
+  int32_t* sel = a.selected + (static_cast<int64_t>(bh) * a.n_blocks + row) * a.max_k;
+  const int32_t* cand = a.cand + static_cast<int64_t>(bi) * a.n_cand;
+  const float* proxy = a.proxy + static_cast<int64_t>(bi) * a.n_cand * a.groups;
+  const int32_t removed = sel[slot];
+  // the removed block's candidate position (its first occurrence), if any
+  for (int l = t; l < a.n_cand; l += kRouteThreads)
+    if (cand[l] == removed) atomicMin(&s_hit, l);
+  __syncthreads();
+  const int hit = s_hit;
+  if (t < a.groups) {
+    const float rem = hit < a.n_cand ? proxy[static_cast<int64_t>(hit) * a.groups + t] : 0.0f;
+    const float add = proxy[static_cast<int64_t>(pos) * a.groups + t];
+    a.error[static_cast<int64_t>(bi) * a.groups + t] += rem - add;
+  }
+  if (t == 0) {
+    const int32_t added = cand[pos];
+    sel[slot] = added;
+    int32_t* rec = a.state + 2 + 6 * swaps;
+    rec[0] = bh;
+    rec[1] = row;
+    rec[2] = slot;
+    rec[3] = removed;
+    rec[4] = added;
+    rec[5] = __float_as_int(-bv);
+    a.state[0] = swaps + 1;
+  }
+}
+
+// The checks at the end of a refine (P/fc_pasm_swap_routing.py:983-1033), per
+// (bh, row) over the first count entries of the row before
+// (base) and after (sel) the refinement, summed into out (int32, zero before):
+// [0] rows whose memory-bank count changed, [1] rows with a repeated block,
+// [2] local edges the rows keep, [3] rows whose current-bank blocks changed,
+// [4] / [5] memory-bank entries before / after, [6] max_k - the smallest
+// count, [7] the largest count, [8] the count sum, [9] the local edges of the
+// stencil over all rows (what [2] must equal).
+struct CheckArgs {
+  const int32_t* base;     // [n_bh, n_blocks, max_k]
+  const int32_t* sel;      // [n_bh, n_blocks, max_k]
+  const int32_t* counts;   // [n_bh, n_blocks]
+  const uint8_t* local;    // [n_blocks, n_blocks]
+  int n_blocks, memory_blocks, max_k;
+  int32_t* out;
+};
+
+// One workgroup per (bh, run of kCheckRows rows), one wavefront per row at a
+// time (bitmaps in LDS per wavefront); the sums meet in LDS, then ten global
+// atomics per workgroup.
+constexpr int kCheckRows = 16;
+__global__ void __launch_bounds__(kRouteThreads)
+route_check_kernel(CheckArgs a) {
+  constexpr int kWords = kRouteMaxBlocks / 32;
+  constexpr int kWaves = kRouteThreads / kWave;
+  __shared__ uint32_t s_seen[kWaves][kWords];   // blocks kept after
+  __shared__ uint32_t s_cur0[kWaves][kWords];   // current-bank blocks kept before
+  __shared__ int s_acc[10];
+  const int N = a.n_blocks, M = a.memory_blocks, K = a.max_k;
+  const int runs = (N + kCheckRows - 1) / kCheckRows;
+  const int64_t bh = blockIdx.x / runs;
+  const int row0 = static_cast<int>(blockIdx.x % runs) * kCheckRows;
+  const int row_end = min(row0 + kCheckRows, N);
+  const int t = threadIdx.x, lane = t % kWave, wave = t / kWave;
+  if (t < 10) s_acc[t] = 0;
+  int acc[10] = {0, 0, 0, 0, 0, 0, 0, 0, 0, 0};
+  for (int row = row0 + wave; row < row_end; row += kWaves) {
+    for (int w = lane; w < kWords; w += kWave) { s_seen[wave][w] = 0u; s_cur0[wave][w] = 0u; }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    const int cnt = min(max(a.counts[bh * N + row], 0), K);
+    const int32_t* base = a.base + (bh * N + row) * static_cast<int64_t>(K);
+    const int32_t* sel = a.sel + (bh * N + row) * static_cast<int64_t>(K);
+    const uint8_t* loc = a.local + static_cast<int64_t>(row) * N;
+    int hist0 = 0, hist1 = 0, kept_local = 0, dup = 0, cur0 = 0, cur1 = 0, stencil = 0;
+    for (int s = lane; s < cnt; s += kWave) {
+      const int32_t b0 = base[s], b1 = sel[s];
+      hist0 += b0 >= 0 && b0 < M;
+      hist1 += b1 >= 0 && b1 < M;
+      if (b0 >= M && b0 < N) {
+        atomicOr(&s_cur0[wave][b0 / 32], 1u << (b0 % 32));
+        ++cur0;
+      }
+      if (b1 >= 0 && b1 < N) {
+        kept_local += loc[b1] != 0;
+        const uint32_t bit = 1u << (b1 % 32);
+        dup += (atomicOr(&s_seen[wave][b1 / 32], bit) & bit) != 0u;
+        cur1 += b1 >= M;
+      }
+    }
+    for (int j = lane; j < N; j += kWave) stencil += loc[j] != 0;
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    // current-bank blocks after, as a bitmap, against those before
+    int cur_diff = 0;
+    for (int w = lane; w < kWords; w += kWave) {
+      uint32_t after = s_seen[wave][w];
+      const int lo = w * 32;
+      if (lo + 32 <= M) after = 0u;
+      else if (lo < M) after &= ~((1u << (M - lo)) - 1u);
+      cur_diff += after != s_cur0[wave][w];
+    }
+    hist0 = wave_sum_i(hist0); hist1 = wave_sum_i(hist1);
+    dup = wave_sum_i(dup); cur0 = wave_sum_i(cur0); cur1 = wave_sum_i(cur1);
+    cur_diff = wave_sum_i(cur_diff);
+    acc[0] += hist0 != hist1;
+    acc[1] += dup != 0;
+    acc[2] += kept_local;  // summed over lanes below
+    acc[3] += (cur_diff != 0 || cur0 != cur1);
+    acc[4] += hist0;
+    acc[5] += hist1;
+    acc[6] = max(acc[6], K - cnt);
+    acc[7] = max(acc[7], cnt);
+    acc[8] += cnt;
+    acc[9] += stencil;  // summed over lanes below
+    __builtin_amdgcn_wave_barrier();
+  }
+  acc[2] = wave_sum_i(acc[2]);
+  acc[9] = wave_sum_i(acc[9]);
+  __syncthreads();
+  if (lane == 0) {
+#pragma unroll
+    for (int i = 0; i < 10; ++i) {
+      if (i == 6 || i == 7) atomicMax(&s_acc[i], acc[i]);
+      else atomicAdd(&s_acc[i], acc[i]);
+    }
+  }
+  __syncthreads();
+  if (t < 10) {
+    if (t == 6 || t == 7) atomicMax(&a.out[t], s_acc[t]);
+    else atomicAdd(&a.out[t], s_acc[t]);
   }
 }
 
@@ -397,5 +631,43 @@ extern "C" int rcsa_route_best_swap(const float* proxy, const int32_t* cand, con
   const int64_t grid = n_bh * (n_blocks - memory_blocks);
   const size_t lds = static_cast<size_t>(max_k * sketch_groups) * sizeof(float);
   route_swap_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kRouteThreads), lds, stream>>>(a);
+  return launch_status();
+}
+
+extern "C" int rcsa_route_apply_swap(const float* best, const int32_t* best_flat,
+                                     const int32_t* cand, const float* proxy, int32_t* selected,
+                                     float* error, int32_t* state, int64_t n_bh,
+                                     int64_t n_blocks, int64_t memory_blocks, int64_t max_k,
+                                     int64_t n_cand, int64_t sketch_groups, int64_t max_swaps,
+                                     int64_t max_records, float eps, hipStream_t stream) {
+  if (!best || !best_flat || !cand || !proxy || !selected || !error || !state)
+    return RCSA_ERR_NULL;
+  int st = route_shapes(n_bh, n_blocks, memory_blocks, max_k, n_cand, sketch_groups, 1);
+  if (st) return st;
+  if (max_swaps < 0 || max_records <= 0 || max_records > 64 || !(eps >= 0.0f))
+    return RCSA_ERR_SHAPE;
+  const ApplyArgs a{best, best_flat, cand, proxy, selected, error, state,
+                    static_cast<int>(n_bh), static_cast<int>(n_blocks),
+                    static_cast<int>(memory_blocks), static_cast<int>(max_k),
+                    static_cast<int>(n_cand), static_cast<int>(sketch_groups),
+                    static_cast<int>(max_swaps < (int64_t{1} << 30) ? max_swaps : 0),
+                    static_cast<int>(max_records), eps};
+  route_apply_kernel<<<dim3(1), dim3(kRouteThreads), 0, stream>>>(a);
+  return launch_status();
+}
+
+extern "C" int rcsa_route_check(const int32_t* base, const int32_t* selected,
+                                const int32_t* counts, const uint8_t* local, int64_t n_bh,
+                                int64_t n_blocks, int64_t memory_blocks, int64_t max_k,
+                                int32_t* out, hipStream_t stream) {
+  if (!base || !selected || !counts || !local || !out) return RCSA_ERR_NULL;
+  if (n_bh <= 0 || n_blocks <= 0 || n_blocks > kRouteMaxBlocks) return RCSA_ERR_SHAPE;
+  if (memory_blocks < 0 || memory_blocks > n_blocks || max_k <= 0) return RCSA_ERR_SHAPE;
+  if (n_bh * n_blocks >= (int64_t{1} << 31) || n_bh * n_blocks * max_k >= (int64_t{1} << 31))
+    return RCSA_ERR_SHAPE;
+  const CheckArgs a{base, selected, counts, local, static_cast<int>(n_blocks),
+                    static_cast<int>(memory_blocks), static_cast<int>(max_k), out};
+  const int64_t grid = n_bh * ((n_blocks + kCheckRows - 1) / kCheckRows);
+  route_check_kernel<<<dim3(static_cast<unsigned>(grid)), dim3(kRouteThreads), 0, stream>>>(a);
   return launch_status();
 }

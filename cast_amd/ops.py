@@ -772,6 +772,63 @@ def route_best_swap(proxy: torch.Tensor, cand: torch.Tensor, local: torch.Tensor
     return best, flat
 
 
+def route_apply_swap(best: torch.Tensor, flat: torch.Tensor, cand: torch.Tensor,
+                     proxy: torch.Tensor, selected: torch.Tensor, error: torch.Tensor,
+                     state: torch.Tensor, *, memory_blocks: int, max_swaps: int, eps: float
+                     ) -> None:
+    """One swap round's decision and exchange on the device (``rcsa_route_apply_swap``,
+    P/fc_pasm_swap_routing.py:935-977): the strongest row's exchange is written into
+    ``selected`` (int32 [B, H, N, K], in place) and its error row ``error``
+    (fp32 [B*H, R, G], in place) unless ``state`` (int32 [2 + 6 * rounds], zero
+    before the first round) says the refinement stopped, ``max_swaps`` (> 0) swaps
+    are done or the best value is not below ``-eps``.  Nothing is read back."""
+    fn = "route_apply_swap"
+    _require_cuda(fn, best, flat, cand, proxy, selected, error, state)
+    BH, R, L, G = proxy.shape
+    B, H, N, K = selected.shape
+    if (best.shape != (BH, R) or flat.shape != (BH, R) or cand.shape != (BH, R, L)
+            or error.shape != (BH, R, G) or B * H != BH or N - int(memory_blocks) != R):
+        raise ValueError(f"{fn}: inconsistent best/candidate/selection shapes")
+    for name, t, dt in (("best", best, torch.float32), ("flat", flat, torch.int32),
+                        ("cand", cand, torch.int32), ("proxy", proxy, torch.float32),
+                        ("selected", selected, torch.int32), ("error", error, torch.float32),
+                        ("state", state, torch.int32)):
+        if t.dtype != dt or not t.is_contiguous():
+            raise ValueError(f"{fn}: {name} must be contiguous {dt}")
+    records = (state.numel() - 2) // 6
+    if records < 1 or state.numel() != 2 + 6 * records:
+        raise ValueError(f"{fn}: state must hold 2 + 6 * rounds int32 entries")
+    check(_lib.load().rcsa_route_apply_swap(
+        best.data_ptr(), flat.data_ptr(), cand.data_ptr(), proxy.data_ptr(), selected.data_ptr(),
+        error.data_ptr(), state.data_ptr(), BH, N, int(memory_blocks), K, L, G, int(max_swaps),
+        records, float(eps), _stream()), fn)
+
+
+def route_check(base: torch.Tensor, selected: torch.Tensor, counts: torch.Tensor,
+                local: torch.Tensor, *, memory_blocks: int) -> torch.Tensor:
+    """The checks at the end of a refine as device sums (``rcsa_route_check``,
+    P/fc_pasm_swap_routing.py:983-1033): int32 [10] = (rows whose memory-bank count
+    changed, rows with a repeated block, local edges kept, rows whose current-bank
+    blocks changed, memory-bank entries before, after, max_k - smallest count,
+    largest count, count sum, local edges of the stencil over all rows).  Nothing
+    is read back."""
+    fn = "route_check"
+    _require_cuda(fn, base, selected, counts)
+    B, H, N, K = selected.shape
+    if base.shape != selected.shape or counts.shape != (B, H, N) or local.shape != (N, N):
+        raise ValueError(f"{fn}: inconsistent route/count/stencil shapes")
+    dev = selected.device
+    b32 = base.to(torch.int32).contiguous()
+    s32 = selected.to(torch.int32).contiguous()
+    c32 = counts.to(torch.int32).contiguous()
+    loc = _bytes_mask(local, dev)
+    out = torch.zeros(10, device=dev, dtype=torch.int32)
+    check(_lib.load().rcsa_route_check(b32.data_ptr(), s32.data_ptr(), c32.data_ptr(),
+                                       loc.data_ptr(), B * H, N, int(memory_blocks), K,
+                                       out.data_ptr(), _stream()), fn)
+    return out
+
+
 def quantize_rows_int8(x: torch.Tensor):
     """Per-token symmetric int8 quantisation of ``x [..., C]`` (``rcsa_quantize_rows_int8``):
     (q int8 [M, C], scale fp32 [M]) with M the product of the leading dims."""

@@ -24,9 +24,11 @@ reference's g = 0 propagation).  The historical-only ablation is not built.
 from __future__ import annotations
 
 import math
+import struct
 from dataclasses import dataclass
 from typing import Any, Callable, Optional
 
+import numpy as np
 import torch
 
 from . import ops
@@ -92,6 +94,7 @@ class FCPASMSwapRouter:
         self.config = config
         self.operator = operator
         self._records: list[dict[str, Any]] = []
+        self._plans: dict = {}
 
     # ---- the objective over the current cells (torch on the device) ----
     def _matrix(self, transport, pair, shape, exponent, device):
@@ -103,10 +106,6 @@ class FCPASMSwapRouter:
                 if m is not None:
                     return m.to(device=device, dtype=torch.float32)
         return None
-
-    @staticmethod
-    def _f32(x: float) -> torch.Tensor:
-        return torch.tensor(x, dtype=torch.float32)
 
     @staticmethod
     def _cells(frames, group, cells):
@@ -122,86 +121,128 @@ class FCPASMSwapRouter:
         return [(int(l), int(r)) for l, r in zip(frames, frames[1:])
                 if (l < boundary) == (r < boundary) and r - l > 1]
 
-    def _terms(self, error, cells, spatial, frames, group, boundary, transport):
-        """Quadratic coefficient (per row) and linear term (per row and group)
-        of the objective at ``error`` (P/fc_pasm_swap_routing.py:414-547)."""
+    def _plan(self, cells, spatial, frames, group, boundary, transport, device):
+        """The objective's structure over the current cells
+        (P/fc_pasm_swap_routing.py:414-614), built once per refine on the host:
+
+        * anchor counts and every pair propagated with the identity (g = 0) fold
+          into per-cell quadratic coefficients and weights of the cells' squared
+          error norms and cross products (the value), and per-pair cross weights
+          (the linear term), fp32 like the reference's scalar products;
+        * a pair with a transport operator keeps its skipped frames' operators
+          stacked, ((1 - a) T^a, a T^-(1-a)) [frames, S, S], for batched products.
+
+        Plans of identity-only objectives are cached per geometry."""
         cfg = self.config
-        BH, rows, G = error.shape
-        view = error.reshape(BH, cells, spatial, G)
+        key = (cells, spatial, tuple(frames), group, boundary, str(device),
+               cfg.lambda_anchor, cfg.lambda_reconstruction)
+        if transport is None and key in self._plans:
+            return self._plans[key]
+        f32 = np.float32
         cell = self._cells(frames, group, cells)
         count = [0.0] * cells
         for f in frames:
             count[cell[int(f)]] += 1.0
-        coef = (torch.tensor(count, dtype=torch.float32, device=error.device)[:, None]
-                .expand(-1, spatial).clone() * cfg.lambda_anchor)
-        lin = torch.zeros_like(view)
+        la, lr = cfg.lambda_anchor, cfg.lambda_reconstruction
+        coef = [f32(c) * f32(la) for c in count]
+        weight = np.zeros((cells, cells), dtype=np.float64)
+        for c in range(cells):
+            weight[c, c] += la * count[c]
+        cross, stacks = [], []
         used = False
         shape = self._grid(transport, spatial)
         for left, right in self._pairs(frames, boundary):
             lc, rc = cell[left], cell[right]
-            el, er = view[:, lc], view[:, rc]
-            for target in range(left + 1, right):
-                a = float(target - left) / float(right - left)
-                lm = self._matrix(transport, (left, right), shape, a, error.device)
-                rm = self._matrix(transport, (left, right), shape, -(1.0 - a), error.device)
-                lam = cfg.lambda_reconstruction
-                if lm is None and rm is None:
-                    # identity operators (g = 0): the same products in fp32 scalars
-                    wl, wr, la = self._f32(1.0 - a), self._f32(a), self._f32(lam)
+            alphas = [float(t - left) / float(right - left) for t in range(left + 1, right)]
+            mats = [(self._matrix(transport, (left, right), shape, a, device),
+                     self._matrix(transport, (left, right), shape, -(1.0 - a), device))
+                    for a in alphas]
+            if all(lm is None and rm is None for lm, rm in mats):
+                x = f32(0.0)
+                for a in alphas:
+                    wl, wr, lam = f32(1.0 - a), f32(a), f32(lr)
                     if lc == rc:
                         c = wl + wr
-                        coef[lc] += float(la * (c * c))
+                        coef[lc] += lam * (c * c)
                     else:
-                        coef[lc] += float(la * (wl * wl))
-                        coef[rc] += float(la * (wr * wr))
-                        x = float(la * (wl * wr))
-                        lin[:, lc] += x * er
-                        lin[:, rc] += x * el
-                    continue
-                used = True
-                eye = torch.eye(spatial, device=error.device, dtype=torch.float32)
-                lm = eye if lm is None else lm
-                rm = eye if rm is None else rm
-                lo, ro = (1.0 - a) * lm, a * rm
-                if lc == rc:
-                    comb = lo + ro
-                    hess = lam * (comb.T @ comb)
-                    dg = torch.diagonal(hess)
-                    coef[lc] += dg
-                    lin[:, lc] += torch.einsum("st,btg->bsg", hess, el) - dg[None, :, None] * el
-                else:
-                    hl, hr, hx = lam * (lo.T @ lo), lam * (ro.T @ ro), lam * (lo.T @ ro)
-                    dl, dr = torch.diagonal(hl), torch.diagonal(hr)
-                    coef[lc] += dl
-                    coef[rc] += dr
-                    lin[:, lc] += (torch.einsum("st,btg->bsg", hl, el) - dl[None, :, None] * el
-                                   + torch.einsum("st,btg->bsg", hx, er))
-                    lin[:, rc] += (torch.einsum("st,btg->bsg", hr, er) - dr[None, :, None] * er
-                                   + torch.einsum("st,btg->bsg", hx.T, el))
-        return coef.reshape(rows), lin.reshape(BH, rows, G), used
+                        coef[lc] += lam * (wl * wl)
+                        coef[rc] += lam * (wr * wr)
+                        x += lam * (wl * wr)
+                    weight[lc, lc] += lr * (1.0 - a) ** 2
+                    weight[rc, rc] += lr * a * a
+                    weight[lc, rc] += lr * a * (1.0 - a)
+                    weight[rc, lc] += lr * a * (1.0 - a)
+                if lc != rc:
+                    cross.append((lc, rc, float(x)))
+                continue
+            used = True
+            eye = torch.eye(spatial, device=device, dtype=torch.float32)
+            lo = torch.stack([(1.0 - a) * (eye if lm is None else lm)
+                              for a, (lm, _) in zip(alphas, mats)])
+            ro = torch.stack([a * (eye if rm is None else rm) for a, (_, rm) in zip(alphas, mats)])
+            stacks.append((lc, rc, lo, ro))
 
-    def _value(self, error, cells, spatial, frames, group, boundary, transport):
-        """The objective (P/fc_pasm_swap_routing.py:550-614)."""
-        cfg = self.config
+        def dev32(a):
+            return torch.from_numpy(np.asarray(a, dtype=np.float32)).pin_memory().to(
+                device, non_blocking=True)
+        diag = [weight[c, c] for c in range(cells)]
+        cross_w = [(c, d, weight[c, d] + weight[d, c]) for c in range(cells)
+                   for d in range(c + 1, cells) if weight[c, d] + weight[d, c] != 0.0]
+        plan = {"coef": dev32(coef).repeat_interleave(spatial), "diag": dev32(diag),
+                "cross_value": cross_w, "cross": cross, "stacks": stacks, "used": used}
+        if transport is None:
+            self._plans[key] = plan
+        return plan
+
+    def _terms(self, error, cells, spatial, plan):
+        """Quadratic coefficient (per row) and linear term (per row and group)
+        of the objective at ``error`` (P/fc_pasm_swap_routing.py:414-547)."""
+        lam = self.config.lambda_reconstruction
         BH, rows, G = error.shape
         view = error.reshape(BH, cells, spatial, G)
-        cell = self._cells(frames, group, cells)
-        count = [0.0] * cells
-        for f in frames:
-            count[cell[int(f)]] += 1.0
-        cw = torch.tensor(count, dtype=torch.float32, device=error.device)
-        value = cfg.lambda_anchor * (view.square() * cw[None, :, None, None]).sum()
-        shape = self._grid(transport, spatial)
-        for left, right in self._pairs(frames, boundary):
-            el, er = view[:, cell[left]], view[:, cell[right]]
-            for target in range(left + 1, right):
-                a = float(target - left) / float(right - left)
-                lm = self._matrix(transport, (left, right), shape, a, error.device)
-                rm = self._matrix(transport, (left, right), shape, -(1.0 - a), error.device)
-                pl = el if lm is None else torch.einsum("st,btg->bsg", lm, el)
-                pr = er if rm is None else torch.einsum("st,btg->bsg", rm, er)
-                prop = (1.0 - a) * pl + a * pr
-                value = value + cfg.lambda_reconstruction * prop.square().sum()
+        lin = torch.zeros_like(view)
+        for lc, rc, x in plan["cross"]:
+            lin[:, lc].add_(view[:, rc], alpha=x)
+            lin[:, rc].add_(view[:, lc], alpha=x)
+        coef = plan["coef"]
+        if plan["stacks"]:
+            coef = coef.clone().reshape(cells, spatial)
+        for lc, rc, lo, ro in plan["stacks"]:
+            el, er = view[:, lc], view[:, rc]
+            if lc == rc:
+                comb = lo + ro
+                hess = lam * torch.einsum("tka,tkb->ab", comb, comb)
+                dg = torch.diagonal(hess)
+                coef[lc] += dg
+                lin[:, lc] += torch.einsum("st,btg->bsg", hess, el) - dg[None, :, None] * el
+            else:
+                hl = lam * torch.einsum("tka,tkb->ab", lo, lo)
+                hr = lam * torch.einsum("tka,tkb->ab", ro, ro)
+                hx = lam * torch.einsum("tka,tkb->ab", lo, ro)
+                dl, dr = torch.diagonal(hl), torch.diagonal(hr)
+                coef[lc] += dl
+                coef[rc] += dr
+                lin[:, lc] += (torch.einsum("st,btg->bsg", hl, el) - dl[None, :, None] * el
+                               + torch.einsum("st,btg->bsg", hx, er))
+                lin[:, rc] += (torch.einsum("st,btg->bsg", hr, er) - dr[None, :, None] * er
+                               + torch.einsum("st,btg->bsg", hx.T, el))
+        return coef.reshape(rows), lin.reshape(BH, rows, G)
+
+    def _value(self, error, cells, spatial, plan):
+        """The objective (P/fc_pasm_swap_routing.py:550-614): the anchor and
+        identity-propagated terms as weighted squared norms and cross products
+        of the cells' errors, the transported frames through their stacked
+        operators."""
+        BH, rows, G = error.shape
+        view = error.reshape(BH, cells, spatial, G)
+        value = (plan["diag"] * view.square().sum(dim=(0, 2, 3))).sum()
+        for c, d, wcd in plan["cross_value"]:
+            value = value + wcd * (view[:, c] * view[:, d]).sum()
+        lam = self.config.lambda_reconstruction
+        for lc, rc, lo, ro in plan["stacks"]:
+            prop = (torch.einsum("tuv,bvg->tbug", lo, view[:, lc])
+                    + torch.einsum("tuv,bvg->tbug", ro, view[:, rc]))
+            value = value + lam * prop.square().sum()
         return value
 
     def _fallback(self, layer_index, reason, **extra):
@@ -276,78 +317,76 @@ class FCPASMSwapRouter:
                     matching_transport_affinity=affinity,
                     min_pair_transport_affinity=cfg.min_pair_transport_affinity,
                     pair_gate_cells=0, fc_cache_used=bool(matching))
-            gate = cg.repeat_interleave(spatial).to(score.device)
+            gate = cg.repeat_interleave(spatial).pin_memory().to(score.device, non_blocking=True)
 
         dev = score.device
         K = selected.shape[-1]
         cnt = counts.clamp(0, K).to(torch.int32)
         sel = selected.to(torch.int32).contiguous()
-        valid = torch.arange(K, device=dev)[None, None, None] < cnt[..., None]
-        hist_before = ((sel < M) & valid).sum(-1)
-        max_swappable = int(cnt.max().item())
-        if max_swappable == 0:
-            return baseline, self._fallback(layer_index, "no_swappable_kv_selected")
-        L = min(N, cfg.candidate_multiplier * max_swappable)
+        if sel.data_ptr() == selected.data_ptr():
+            sel = sel.clone()  # the caller's route stays as it was
+        # Candidates for the widest possible row (the list width bounds every
+        # count): each row still uses only its first min(mult * count, N), so the
+        # result is that of the reference's min(N, mult * max count) candidates
+        # without reading the counts back.
+        L = min(N, cfg.candidate_multiplier * K)
         cand, proxy, error = ops.route_proxy(
             score, pooled_value, local, sel, cnt, memory_blocks=M, n_cand=L,
             cand_mult=cfg.candidate_multiplier, sketch_groups=cfg.sketch_groups)
-        geo = (cells, spatial, frames, int(temporal_group_size), int(current_boundary), transport)
-        obj_before = self._value(error, *geo)
-        cache_used = bool(matching)
-        swaps, improvements = 0, []
-        for _ in range(cfg.num_swap_rounds):
-            coef, lin, used = self._terms(error, *geo)
-            cache_used = cache_used or used
+        plan = self._plan(cells, spatial, frames, int(temporal_group_size),
+                          int(current_boundary), transport, dev)
+        obj_before = self._value(error, cells, spatial, plan)
+        cache_used = bool(matching) or plan["used"]
+        rounds = cfg.num_swap_rounds
+        # swap count, stop flag and the applied swaps, written by the device
+        state = torch.zeros(2 + 6 * rounds, device=dev, dtype=torch.int32)
+        for _ in range(rounds):
+            coef, lin = self._terms(error, cells, spatial, plan)
             best, flat = ops.route_best_swap(proxy, cand, local, sel, cnt, coef, lin, error,
                                              memory_blocks=M, cand_mult=cfg.candidate_multiplier,
                                              same_bank=cfg.same_bank_only, row_gate=gate)
-            strongest = int(torch.argmin(best.reshape(-1)).item())
-            value = float(best.reshape(-1)[strongest].item())
-            if cfg.max_swaps_per_call and swaps >= cfg.max_swaps_per_call:
-                break
-            if not value < -cfg.swap_eps:
-                break
-            bh, rr = divmod(strongest, rows)
-            fl = int(flat[bh, rr].item())
-            slot, pos = divmod(fl, L)
-            b, h = divmod(bh, H)
-            row = M + rr
-            removed = sel[b, h, row, slot]
-            hit = (cand[bh, rr] == removed).nonzero()
-            rem = proxy[bh, rr, int(hit[0, 0])] if hit.numel() else torch.zeros_like(proxy[bh, rr, 0])
-            sel[b, h, row, slot] = cand[bh, rr, pos]
-            error = error.clone()
-            error[bh, rr] += rem - proxy[bh, rr, pos]
-            swaps += 1
-            improvements.append(-value)
-
-        valid_final = valid
-        hist_after = ((sel < M) & valid_final).sum(-1)
-        if cfg.same_bank_only and not torch.equal(hist_before, hist_after):
+            ops.route_apply_swap(best, flat, cand, proxy, sel, error, state, memory_blocks=M,
+                                 max_swaps=cfg.max_swaps_per_call, eps=cfg.swap_eps)
+        # the checks at the end (P/fc_pasm_swap_routing.py:983-1033) as device
+        # sums, read back once with the objective and the applied swaps
+        checks = ops.route_check(baseline, sel, cnt, local, memory_blocks=M)
+        obj_after = self._value(error, cells, spatial, plan)
+        host = torch.cat([checks.double(), torch.stack([obj_before, obj_after]).double(),
+                          state.double()]).cpu()  # the one read-back of a refine
+        vals = [int(x) for x in host[:10].tolist()]
+        before_f, after_f = float(host[10]), float(host[11])
+        st = [int(x) for x in host[12:].tolist()]
+        swaps = st[0]
+        if vals[7] == 0:  # no row keeps a block
+            return baseline, self._fallback(layer_index, "no_swappable_kv_selected")
+        if cfg.same_bank_only and vals[0]:
             raise RuntimeError("same-bank FC-PASM routing changed Memory KV counts")
-        s64 = sel.long()
-        # duplicates among a row's kept entries: equal neighbours once sorted
-        # (padding slots become distinct values past every block)
-        pad = N + torch.arange(K, device=dev)
-        srt = torch.where(valid_final, s64, pad).sort(dim=-1).values
-        if bool((srt[..., 1:] == srt[..., :-1]).any()):
+        if vals[1]:
             raise RuntimeError("FC-PASM routing emitted duplicate keys")
-        loc = local.to(device=dev, dtype=torch.bool)
-        final_local = torch.gather(loc[None, None].expand(B, H, -1, -1), -1,
-                                   s64.clamp_min(0)) & valid_final
-        if int(final_local.sum().item()) != int(loc.sum().item()) * B * H:
+        if vals[2] != vals[9]:
             raise RuntimeError("FC-PASM routing removed a protected local edge")
-        obj_after = self._value(error, *geo)
-        if bool(obj_after > obj_before + 1e-5 * obj_before.abs().clamp_min(1.0)):
+        if after_f > before_f + 1e-5 * max(abs(before_f), 1.0):
             raise RuntimeError("FC-PASM swap increased its refinement objective")
+        hb, ha = vals[4], vals[5]
+        kmin, kmax, ksum, max_swappable = K - vals[6], vals[7], vals[8], vals[7]
+        cur_unchanged = vals[3] == 0
+        chosen = []
+        for i in range(swaps):
+            r = st[2 + 6 * i: 8 + 6 * i]
+            b, h = divmod(r[0], H)
+            imp = struct.unpack("<f", struct.pack("<i", r[5]))[0]
+            chosen.append({"b": b, "h": h, "row": r[1], "slot": r[2], "removed": r[3],
+                           "added": r[4], "improvement": imp})
         record = {
             "layer_index": int(layer_index), "status": "refined",
-            "candidate_multiplier": cfg.candidate_multiplier, "candidate_max": L,
+            "candidate_multiplier": cfg.candidate_multiplier,
+            "candidate_max": min(N, cfg.candidate_multiplier * max_swappable),
             "swap_rounds": cfg.num_swap_rounds, "max_swaps_per_call": cfg.max_swaps_per_call,
-            "swap_count": swaps, "objective_before": obj_before.detach(),
-            "objective_after": obj_after.detach(),
-            "objective_improvement": (obj_before - obj_after).detach(),
-            "average_swap_improvement": (sum(improvements) / swaps if swaps else 0.0),
+            "swap_count": swaps, "objective_before": before_f,
+            "objective_after": after_f,
+            "objective_improvement": before_f - after_f,
+            "average_swap_improvement": (sum(c["improvement"] for c in chosen) / swaps
+                                         if swaps else 0.0),
             "anchor_term_weight": cfg.lambda_anchor,
             "reconstruction_term_weight": cfg.lambda_reconstruction,
             "reconstruction_terms": sum(max(0, r - l - 1) for l, r in zip(frames, frames[1:])
@@ -356,11 +395,10 @@ class FCPASMSwapRouter:
             "min_pair_transport_affinity": cfg.min_pair_transport_affinity,
             "pair_gate_cells": gate_cells, "g0_fallback": not cache_used, "fixed_budget": True,
             "historical_only": cfg.historical_only, "same_bank_only": cfg.same_bank_only,
-            "historical_budget_before": int(hist_before.sum().item()),
-            "historical_budget_after": int(hist_after.sum().item()),
-            "minimum_k": int(counts.min().item()), "maximum_k": int(counts.max().item()),
-            "budget_before": int(counts.sum().item()), "budget_after": int(counts.sum().item()),
-            "unique_indices": True, "local_support_preserved": True,
+            "historical_budget_before": hb, "historical_budget_after": ha,
+            "current_kv_support_unchanged": bool(cur_unchanged),
+            "minimum_k": kmin, "maximum_k": kmax, "budget_before": ksum, "budget_after": ksum,
+            "unique_indices": True, "local_support_preserved": True, "swaps": chosen,
         }
         self._records.append(record)
         return sel.to(selected.dtype), record

@@ -514,6 +514,43 @@ int rcsa_route_best_swap(const float* proxy, const int32_t* cand, const uint8_t*
                          int same_bank, float* best, int32_t* best_flat, hipStream_t stream);
 
 /*
+ * One swap round's decision and exchange on the device, replacing the host
+ * argmin / scatter / error update of FCPASMLocalCoordinateSwapRouter.refine
+ * (P/fc_pasm_swap_routing.py:935-977) so that a refine reads nothing back until
+ * its record.  One workgroup: the strongest row is the first minimum of best
+ * [n_bh * rows] (rows = n_blocks - memory_blocks); unless state[1] is set, the
+ * swap limit max_swaps (> 0) is reached or that minimum is not below -eps, its
+ * exchange best_flat = slot * n_cand + l writes cand[l] into the slot of
+ * selected [n_bh][n_blocks][max_k] and adds (the removed block's proxy, zero
+ * when it is not a candidate of the row) - proxy[l] to the row's error
+ * [n_bh][rows][sketch_groups]; otherwise it sets state[1] (stopped).
+ * state: int32 [2 + 6 * max_records], zero before the first round:
+ * [0] swaps applied, [1] stopped, then per swap (bh, row, slot, removed block,
+ * added block, improvement -best as float bits).  max_records <= 64.
+ */
+int rcsa_route_apply_swap(const float* best, const int32_t* best_flat, const int32_t* cand,
+                          const float* proxy, int32_t* selected, float* error, int32_t* state,
+                          int64_t n_bh, int64_t n_blocks, int64_t memory_blocks, int64_t max_k,
+                          int64_t n_cand, int64_t sketch_groups, int64_t max_swaps,
+                          int64_t max_records, float eps, hipStream_t stream);
+
+/*
+ * The checks at the end of a refine (P/fc_pasm_swap_routing.py:983-1033) as
+ * device sums, so that a refine reads its record back once: over every
+ * (bh, row) of the routes before (base) and after (selected), both int32
+ * [n_bh][n_blocks][max_k], first min(max(counts, 0), max_k) entries valid,
+ * local uint8 [n_blocks][n_blocks] (n_blocks <= 1024), out int32 [10], zero on
+ * entry, receives: [0] rows whose memory-bank count changed, [1] rows with a
+ * repeated block, [2] local edges kept, [3] rows whose current-bank blocks
+ * changed, [4]/[5] memory-bank entries before/after, [6] max_k - the smallest
+ * count, [7] the largest count, [8] the count sum, [9] the stencil's local edges
+ * over all rows.
+ */
+int rcsa_route_check(const int32_t* base, const int32_t* selected, const int32_t* counts,
+                     const uint8_t* local, int64_t n_bh, int64_t n_blocks,
+                     int64_t memory_blocks, int64_t max_k, int32_t* out, hipStream_t stream);
+
+/*
  * Shared int8 Q/K/V projection (P/matrix_shared_int8_qkv.py:19-92): the
  * activations are quantised once per token and reused by the three int8
  * projections.  No reference kernel: the reference calls the upstream Matrix
