@@ -31,6 +31,8 @@ SIGNATURES: dict[str, list] = {
     "rcsa_pool_key": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "rcsa_pool_query_key": [_P, _P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                             _P, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P],
+    "rcsa_pool_query_key_value": [_P, _P, _P, c_int] + [_I] * 15 + [_P, _P, _P, _I, _P, _I]
+                                 + [_P] * 9 + [_P],
     "rcsa_block_scores": [_P, _P, _I, _I, _I, _I, _P, _P],
     "rcsa_quantize_key_select": [_P, c_int, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _I,
                                  _P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _P, _P,

@@ -137,7 +137,9 @@ struct Raw8<float> {
 // its row loads first; the block's validity bytes go through LDS while they
 // are in flight, and the per-channel partials are reduced across the row
 // groups of a wavefront by shuffles before one small LDS pass.
-template <typename T, int D, int BS, bool QUANT, bool STATS, bool MAP>
+// NORM false: hat receives the valid-weighted block mean itself (the pooled V
+// of P/matrix_curvature_phase_frame_weave.py:5700), not its normalised direction.
+template <typename T, int D, int BS, bool QUANT, bool STATS, bool MAP, bool NORM = true>
 __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
   constexpr int CPR = D / 8;                 // 16-byte chunks per token row
   constexpr int RG = kPoolThreads / CPR;     // row groups
@@ -230,10 +232,14 @@ __device__ __forceinline__ void pool_tile(const PoolArgs& a, int64_t tile) {
     mean = s / static_cast<float>(n_valid > 0 ? n_valid : 1);
   }
   if (QUANT) amax = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
-  const float norm2 = block_sum(t < D ? mean * mean : 0.0f, s_red);
-  if (t < D) {
-    const float denom = fmaxf(sqrtf(norm2), 1e-12f);
-    a.hat[(bh * a.n_blocks + blk) * D + t] = mean / denom;
+  if constexpr (NORM) {
+    const float norm2 = block_sum(t < D ? mean * mean : 0.0f, s_red);
+    if (t < D) {
+      const float denom = fmaxf(sqrtf(norm2), 1e-12f);
+      a.hat[(bh * a.n_blocks + blk) * D + t] = mean / denom;
+    }
+  } else if (t < D) {
+    a.hat[(bh * a.n_blocks + blk) * D + t] = mean;
   }
 
   if (QUANT) {
@@ -271,11 +277,14 @@ pool_kernel(PoolArgs a) {
 // the rest key tiles.  The short, latency-bound query pass then runs inside
 // the HBM-bound key pass instead of before it.
 // (QS false: the bf16 path's pooling, no query quantiser and no key statistics)
-template <typename T, int D, int BS, bool MAP, bool QS = true>
+// VMEAN: the workgroups past the key tiles (from k_end) pool V tiles into
+// their block means (the router's pooled values), in the same launch.
+template <typename T, int D, int BS, bool MAP, bool QS = true, bool VMEAN = false>
 __global__ void __launch_bounds__(kPoolThreads)
-pool_qk_kernel(PoolArgs q, PoolArgs k, int64_t q_tiles) {
+pool_qk_kernel(PoolArgs q, PoolArgs k, int64_t q_tiles, PoolArgs v, int64_t k_end) {
   if (blockIdx.x < q_tiles) pool_tile<T, D, BS, QS, false, MAP>(q, blockIdx.x);
-  else pool_tile<T, D, BS, false, QS, MAP>(k, blockIdx.x - q_tiles);
+  else if (!VMEAN || blockIdx.x < k_end) pool_tile<T, D, BS, false, QS, MAP>(k, blockIdx.x - q_tiles);
+  else pool_tile<T, D, BS, false, false, MAP, false>(v, blockIdx.x - k_end);
 }
 
 // Cosine scores: one workgroup per (bh, 16 query blocks, 64 key blocks).
@@ -604,15 +613,17 @@ extern "C" int rcsa_pool_key(const void* k, int dtype, int64_t batch, int64_t n_
   return launch_status();
 }
 
-extern "C" int rcsa_pool_query_key(
+static int pool_query_key_impl(
     const void* q, const void* k, int dtype, int64_t batch, int64_t n_heads,
     int64_t n_qblocks, int64_t n_kblocks, int64_t block_size, int64_t head_dim,
     int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
     int64_t k_stride_h, int64_t k_stride_t, const uint8_t* q_valid, const uint8_t* k_valid,
     const int32_t* q_slot_token, int64_t q_src_len, const int32_t* k_slot_token,
     int64_t k_src_len, float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum,
-    float* kmin, float* kmax, uint32_t* block_mask, hipStream_t stream) {
+    float* kmin, float* kmax, uint32_t* block_mask, const void* v, int64_t v_stride_b,
+    int64_t v_stride_h, int64_t v_stride_t, float* vmean, hipStream_t stream) {
   if (!q || !k || !qhat || !khat) return RCSA_ERR_NULL;
+  if ((v == nullptr) != (vmean == nullptr)) return RCSA_ERR_NULL;
   // the quantiser outputs and the key statistics come together or not at all
   const bool qs = q_i8 || q_scale || ksum || kmin || kmax;
   if (qs && !(q_i8 && q_scale && ksum && kmin && kmax)) return RCSA_ERR_NULL;
@@ -628,6 +639,12 @@ extern "C" int rcsa_pool_query_key(
   st = check_pool_shape(dtype, batch, n_heads, n_kblocks, block_size, head_dim, k_stride_b,
                         k_stride_h, k_stride_t);
   if (st) return st;
+  if (v) {  // V: the key layout (slot map, validity, blocks), strides of its own
+    st = check_pool_shape(dtype, batch, n_heads, n_kblocks, block_size, head_dim, v_stride_b,
+                          v_stride_h, v_stride_t);
+    if (st) return st;
+    if (!aligned16(v) || !aligned16(vmean)) return RCSA_ERR_ALIGN;
+  }
   if (!aligned16(q) || !aligned16(k) || (reinterpret_cast<uintptr_t>(q_i8) & 7u))
     return RCSA_ERR_ALIGN;
   if (block_mask && (reinterpret_cast<uintptr_t>(block_mask) & 7u)) return RCSA_ERR_ALIGN;
@@ -636,14 +653,23 @@ extern "C" int rcsa_pool_query_key(
                     q_src_len};
   const PoolArgs ka{k, n_heads, n_kblocks, k_stride_b, k_stride_h, k_stride_t, k_valid, khat,
                     ksum, kmin, kmax, nullptr, nullptr, block_mask, k_slot_token, k_src_len};
+  const PoolArgs va{v, n_heads, n_kblocks, v_stride_b, v_stride_h, v_stride_t, k_valid, vmean,
+                    nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, k_slot_token,
+                    k_src_len};
   const int64_t nbh = batch * n_heads;
   const int64_t q_tiles = nbh * n_qblocks;
-  const dim3 grid(static_cast<unsigned>(q_tiles + nbh * n_kblocks)), block(kPoolThreads);
+  const int64_t k_end = q_tiles + nbh * n_kblocks;
+  const dim3 grid(static_cast<unsigned>(k_end + (v ? nbh * n_kblocks : 0))), block(kPoolThreads);
 #define RCSA_PQK(T_, D_, BS_)                                                     \
-  if (!qs) { if (map) pool_qk_kernel<T_, D_, BS_, true, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles); \
-             else pool_qk_kernel<T_, D_, BS_, false, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles); } \
-  else if (map) pool_qk_kernel<T_, D_, BS_, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles); \
-  else pool_qk_kernel<T_, D_, BS_, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles)
+  if (v) {                                                                        \
+    if (!qs) { if (map) pool_qk_kernel<T_, D_, BS_, true, false, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); \
+               else pool_qk_kernel<T_, D_, BS_, false, false, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); } \
+    else if (map) pool_qk_kernel<T_, D_, BS_, true, true, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); \
+    else pool_qk_kernel<T_, D_, BS_, false, true, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); \
+  } else if (!qs) { if (map) pool_qk_kernel<T_, D_, BS_, true, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); \
+             else pool_qk_kernel<T_, D_, BS_, false, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); } \
+  else if (map) pool_qk_kernel<T_, D_, BS_, true><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end); \
+  else pool_qk_kernel<T_, D_, BS_, false><<<grid, block, 0, stream>>>(qa, ka, q_tiles, va, k_end)
 #define RCSA_PQK_T(T_)                                               \
   if (head_dim == 128 && block_size == 128) { RCSA_PQK(T_, 128, 128); } \
   else if (head_dim == 128) { RCSA_PQK(T_, 128, 64); }                  \
@@ -653,6 +679,39 @@ extern "C" int rcsa_pool_query_key(
 #undef RCSA_PQK_T
 #undef RCSA_PQK
   return launch_status();
+}
+
+extern "C" int rcsa_pool_query_key(
+    const void* q, const void* k, int dtype, int64_t batch, int64_t n_heads,
+    int64_t n_qblocks, int64_t n_kblocks, int64_t block_size, int64_t head_dim,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
+    int64_t k_stride_h, int64_t k_stride_t, const uint8_t* q_valid, const uint8_t* k_valid,
+    const int32_t* q_slot_token, int64_t q_src_len, const int32_t* k_slot_token,
+    int64_t k_src_len, float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum,
+    float* kmin, float* kmax, uint32_t* block_mask, hipStream_t stream) {
+  return pool_query_key_impl(q, k, dtype, batch, n_heads, n_qblocks, n_kblocks, block_size,
+                             head_dim, q_stride_b, q_stride_h, q_stride_t, k_stride_b,
+                             k_stride_h, k_stride_t, q_valid, k_valid, q_slot_token, q_src_len,
+                             k_slot_token, k_src_len, qhat, q_i8, q_scale, khat, ksum, kmin,
+                             kmax, block_mask, nullptr, 0, 0, 0, nullptr, stream);
+}
+
+extern "C" int rcsa_pool_query_key_value(
+    const void* q, const void* k, const void* v, int dtype, int64_t batch, int64_t n_heads,
+    int64_t n_qblocks, int64_t n_kblocks, int64_t block_size, int64_t head_dim,
+    int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t, int64_t k_stride_b,
+    int64_t k_stride_h, int64_t k_stride_t, int64_t v_stride_b, int64_t v_stride_h,
+    int64_t v_stride_t, const uint8_t* q_valid, const uint8_t* k_valid,
+    const int32_t* q_slot_token, int64_t q_src_len, const int32_t* k_slot_token,
+    int64_t k_src_len, float* qhat, int8_t* q_i8, float* q_scale, float* khat, float* ksum,
+    float* kmin, float* kmax, uint32_t* block_mask, float* vmean, hipStream_t stream) {
+  if (!v || !vmean) return RCSA_ERR_NULL;
+  return pool_query_key_impl(q, k, dtype, batch, n_heads, n_qblocks, n_kblocks, block_size,
+                             head_dim, q_stride_b, q_stride_h, q_stride_t, k_stride_b,
+                             k_stride_h, k_stride_t, q_valid, k_valid, q_slot_token, q_src_len,
+                             k_slot_token, k_src_len, qhat, q_i8, q_scale, khat, ksum, kmin,
+                             kmax, block_mask, v, v_stride_b, v_stride_h, v_stride_t, vmean,
+                             stream);
 }
 
 extern "C" int rcsa_block_scores(const float* qhat, const float* khat, int64_t n_bh,

@@ -204,6 +204,63 @@ def pool_query_key(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Te
     return qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask
 
 
+def pool_query_key_value(q: torch.Tensor, q_valid: Optional[torch.Tensor], k: torch.Tensor,
+                         k_valid: Optional[torch.Tensor], v: torch.Tensor, block_size: int, *,
+                         q_slot_token: Optional[torch.Tensor] = None,
+                         k_slot_token: Optional[torch.Tensor] = None, quantize: bool = True):
+    """:func:`pool_query_key` plus the block means of ``v`` in the same launch
+    (``rcsa_pool_query_key_value``): the pooled values ``v_content`` of
+    P/matrix_curvature_phase_frame_weave.py:5696-5700 that the FC-PASM router
+    consumes.  ``v`` has k's layout (packed ``[B, H, L, D]``, or token-major
+    ``[B, L, H, D]`` read through ``k_slot_token``) and shares its validity.
+    Returns pool_query_key's eight outputs and ``vmean`` fp32 ``[B*H, NK, D]``."""
+    fn = "pool_query_key_value"
+    _require_cuda(fn, q, k, v)
+    code = _dtype_code(q, fn)
+    if _dtype_code(k, fn) != code or _dtype_code(v, fn) != code:
+        raise TypeError(f"{fn}: q, k and v must share a dtype")
+    if v.shape != k.shape:
+        raise ValueError(f"{fn}: v {tuple(v.shape)} must have k's shape {tuple(k.shape)}")
+    if (q_slot_token is None) != (k_slot_token is None):
+        raise ValueError(f"{fn}: give both slot maps or neither")
+    if q_slot_token is not None:
+        qm = _slot_map(q_slot_token, block_size, q.device, fn)
+        km = _slot_map(k_slot_token, block_size, k.device, fn)
+        B, H, Lq, D, NQ, q_src, q_strides = _tokens_bhld(q, qm, block_size, fn)
+        Bk, Hk, Lk, Dk, NK, k_src, k_strides = _tokens_bhld(k, km, block_size, fn)
+        _, _, _, _, _, _, v_strides = _tokens_bhld(v, km, block_size, fn)
+    else:
+        qm = km = None
+        q_src = k_src = 0
+        B, H, Lq, D, NQ = _bhld(q, block_size, fn)
+        Bk, Hk, Lk, Dk, NK = _bhld(k, block_size, fn)
+        _bhld(v, block_size, fn)
+        q_strides = (q.stride(0), q.stride(1), q.stride(2))
+        k_strides = (k.stride(0), k.stride(1), k.stride(2))
+        v_strides = (v.stride(0), v.stride(1), v.stride(2))
+    if (Bk, Hk, Dk) != (B, H, D):
+        raise ValueError(f"{fn}: q {tuple(q.shape)} and k {tuple(k.shape)} differ in B, H or D")
+    qv = _valid_u8(q_valid, Lq, q.device, fn)
+    kv = _valid_u8(k_valid, Lk, k.device, fn)
+    f32 = dict(device=q.device, dtype=torch.float32)
+    qhat = torch.empty(B * H, NQ, D, **f32)
+    khat = torch.empty(B * H, NK, D, **f32)
+    vmean = torch.empty(B * H, NK, D, **f32)
+    if quantize:
+        q_i8 = torch.empty(B, H, Lq, D, device=q.device, dtype=torch.int8)
+        q_scale = torch.empty(B * H, NQ, **f32)
+        ksum, kmin, kmax = (torch.empty(B * H, NK, D, **f32) for _ in range(3))
+    else:
+        q_i8 = q_scale = ksum = kmin = kmax = None
+    mask = torch.empty(NK, block_size // 32, device=k.device, dtype=torch.int32)
+    check(_lib.load().rcsa_pool_query_key_value(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), code, B, H, NQ, NK, block_size, D,
+        *q_strides, *k_strides, *v_strides, _ptr(qv), _ptr(kv), _ptr(qm), q_src, _ptr(km),
+        k_src, qhat.data_ptr(), _ptr(q_i8), _ptr(q_scale), khat.data_ptr(), _ptr(ksum),
+        _ptr(kmin), _ptr(kmax), mask.data_ptr(), vmean.data_ptr(), _stream()), fn)
+    return qhat, q_i8, q_scale, khat, ksum, kmin, kmax, mask, vmean
+
+
 def row_budgets(weights: torch.Tensor, total_per_section: int, *, cap: int = 0,
                 target_total: Optional[int] = None) -> torch.Tensor:
     """Per-row budgets on the device: ``budget.apportion_section_matrix(weights, total)``
@@ -256,7 +313,10 @@ def closed_loop_degrees(curvature: torch.Tensor, frames, *, current_temporal_off
         response = response.to(dev).contiguous()
     if feedback_form not in _CL_FEEDBACK:
         raise ValueError(f"unknown control-response feedback {feedback_form!r}")
-    fr = torch.as_tensor(frames).to(device=dev, dtype=torch.int32).reshape(-1).contiguous()
+    fr = torch.as_tensor(frames)
+    if fr.device.type == "cpu":  # pinned, so the copy waits for nothing on the stream
+        fr = fr.to(torch.int32).reshape(-1).contiguous().pin_memory()
+    fr = fr.to(device=dev, dtype=torch.int32, non_blocking=True).reshape(-1).contiguous()
     degrees = torch.empty(int(total_blocks), device=dev, dtype=torch.int32)
     status = torch.empty(1, device=dev, dtype=torch.int32)
     t_src, spatial = curvature.shape

@@ -127,6 +127,29 @@ int rcsa_pool_query_key(const void* q, const void* k, int dtype, int64_t batch,
                         uint32_t* block_mask, hipStream_t stream);
 
 /*
+ * rcsa_pool_query_key plus the block means of V in the same launch:
+ * vmean [batch*n_heads][n_kblocks][head_dim] fp32 (16-byte aligned) =
+ * sum over the valid tokens of the block / max(valid tokens, 1), the pooled
+ * values v_content that the FC-PASM router consumes
+ * (P/matrix_curvature_phase_frame_weave.py:5696-5700).  V shares the key
+ * layout: block count, validity (k_valid) and slot map (k_slot_token,
+ * k_src_len); its strides are its own.  All other arguments and outputs are
+ * those of rcsa_pool_query_key.
+ */
+int rcsa_pool_query_key_value(const void* q, const void* k, const void* v, int dtype,
+                              int64_t batch, int64_t n_heads, int64_t n_qblocks,
+                              int64_t n_kblocks, int64_t block_size, int64_t head_dim,
+                              int64_t q_stride_b, int64_t q_stride_h, int64_t q_stride_t,
+                              int64_t k_stride_b, int64_t k_stride_h, int64_t k_stride_t,
+                              int64_t v_stride_b, int64_t v_stride_h, int64_t v_stride_t,
+                              const uint8_t* q_valid, const uint8_t* k_valid,
+                              const int32_t* q_slot_token, int64_t q_src_len,
+                              const int32_t* k_slot_token, int64_t k_src_len, float* qhat,
+                              int8_t* q_i8, float* q_scale, float* khat, float* ksum,
+                              float* kmin, float* kmax, uint32_t* block_mask, float* vmean,
+                              hipStream_t stream);
+
+/*
  * Row degrees of a compact woven layer under the closed-loop allocator, on the
  * device (no .item() syncs).  Replaces compact_closed_loop_degrees
  * (P/control_response_cwca_attention.py:1188-1363, with _compact_time_cells

@@ -54,6 +54,9 @@ docstring; the pins live in tests/test_oracle_pins.py:
   quantize_rows_int8  error <= scale / 2, the absmax element maps to +-127, zero rows
   int8_linear         pure-Python integer dot products on small shapes; exact
                       int32 accumulation bound; scales factor out
+  compact_cwca_layer  a composition of the functions above (each pinned on its
+                      own); the weights of the pooled V are the pooled-K
+                      weights (pool_blocks' sums over valid slots)
   fc_pasm_refine      the identity (with the reference's fallback reasons) for
                       every missing-transport / disabled case; the chosen swap
                       equals a brute-force search over every admissible
@@ -78,7 +81,7 @@ __all__ = [
     "apportion_section_matrix_f32", "compact_time_cells", "redistribute_compact_capacity",
     "closed_loop_degrees", "relay_layout", "omission_proxy", "route_objective_terms",
     "route_objective_value", "fc_pasm_refine", "transport_maps", "quantize_rows_int8",
-    "int8_linear",
+    "int8_linear", "compact_cwca_layer",
 ]
 
 
@@ -665,6 +668,86 @@ def rcsa_layer(q, k, v, q_valid, k_valid, *, block_size: int, k_select, forced=N
                                     block_n=block_size, heads=heads, qblocks=qblocks)
     res.update(out=out, lse=lse)
     return res
+
+
+def compact_cwca_layer(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                       block_indices: torch.Tensor, *, block_shape, spatial_hw,
+                       active_frame_values, memory_temporal: int, sparse_density: float,
+                       closed_loop: dict, router: Optional[dict] = None,
+                       layer_index: int = 1):
+    """The compact woven layer's attention, composed from the oracle's parts.
+
+    Restates _compact_cwca_attention (P/matrix_curvature_phase_frame_weave.py:
+    5643-6124) with a closed-loop geometry provider: the q/k/v[:, flat] gathers
+    with invalid slots zeroed (:5677-5684), the masked block means (q and k
+    normalised, v not: :5685-5700), the scores (:5701), the local stencil and
+    mean degree (:5703-5731), the layer's degrees (closed_loop_degrees, which
+    includes the saturation of :5807-5817), the top-k of score + 1e6 local at
+    each row's degree (:5829-5832; select_topk), the router's refine with the
+    score it is handed back (score + 1e6 local - 1e6 local in fp32, :6037) when
+    ``router`` is given, then the sparse attention over the packed blocks and
+    the scatter to the token rows (:6086-6095).
+
+    q, k, v: token-major [B, L, H, D]; block_indices: int64 [blocks, block_size]
+    (token or -1).  ``closed_loop``: the keywords of closed_loop_degrees other
+    than the layout's (curvature, current_temporal_offset, source_group,
+    response, response_weight, feedback_form, fixed_query_budget).  ``router``:
+    dict(config=..., transport=..., operator=..., current_boundary=...).
+    Returns dict(out [B, L, H, D] fp32, degrees int64 [blocks], selected
+    [B, H, blocks, max] int64, counts [B, H, blocks], score, vmean, record).
+    """
+    B, L, H, D = q.shape
+    blocks, bs = block_indices.shape
+    flat = block_indices.clamp_min(0).reshape(-1)
+    mask = (block_indices >= 0).reshape(-1)
+
+    def packed(x):
+        xp = x[:, flat].transpose(1, 2).float().clone()
+        xp[:, :, ~mask] = 0
+        return xp
+    qp, kp, vp = packed(q), packed(k), packed(v)
+    qhat, _, _ = pool_blocks(qp, mask, bs)
+    khat, _, _ = pool_blocks(kp, mask, bs)
+    _, vsum, nv = pool_blocks(vp, mask, bs)
+    vmean = vsum / nv.clamp_min(1.0)[None, None, :, None]
+    score = block_scores(qhat, khat)                                 # [B, H, N, N]
+    tt, th, tw = (int(x) for x in block_shape)
+    nh, nw = math.ceil(spatial_hw[0] / th), math.ceil(spatial_hw[1] / tw)
+    spatial = nh * nw
+    frames = [int(f) for f in active_frame_values]
+    memory_frames = sum(1 for f in frames if f < memory_temporal)
+    local = local_stencil(blocks, nh, nw)
+    widest = int(local.sum(dim=-1).max())
+    mean_degree = min(max(widest, int(round(sparse_density * blocks))), blocks)
+    memory_blocks = min(blocks, math.ceil(memory_frames / tt) * spatial)
+    base = max(widest, math.ceil(4 * mean_degree / 5))
+    current_local = [f - memory_temporal for f in frames if f >= memory_temporal]
+    degrees = closed_loop_degrees(
+        closed_loop["curvature"], current_local, compact_group=tt, mean_degree=mean_degree,
+        base_degree=base, total_blocks=blocks, memory_blocks=memory_blocks,
+        layer_index=layer_index,
+        **{kk: vv for kk, vv in closed_loop.items() if kk != "curvature"})
+    sel, cnt = select_topk(score.reshape(B * H, blocks, blocks), degrees, forced=local,
+                           order="rank")
+    selected = sel.reshape(B, H, blocks, -1).long()
+    counts = cnt.reshape(B, H, blocks)
+    record = None
+    if router is not None:
+        bonus = local.to(score.dtype) * 1e6
+        selected, record = fc_pasm_refine(
+            (score + bonus) - bonus, vmean, selected, counts, local,
+            memory_blocks=memory_blocks, spatial_shape=(nh, nw),
+            exact_current_frames=tuple(current_local), temporal_group_size=tt,
+            current_boundary=router.get("current_boundary", 4),
+            transport=router.get("transport"), layer_index=layer_index,
+            config=router["config"], operator=router.get("operator"))
+    out_p, _ = sparse_attention(qp, kp, vp, selected, counts, mask, block_m=bs, block_n=bs)
+    token_to_packed = torch.empty(L, dtype=torch.long)
+    token_to_packed[block_indices.reshape(-1)[mask]] = torch.nonzero(mask).flatten()
+    out = out_p.transpose(1, 2)[:, token_to_packed]
+    return {"out": out, "degrees": degrees, "selected": selected, "counts": counts,
+            "score": score, "vmean": vmean, "record": record, "mean_degree": mean_degree,
+            "memory_blocks": memory_blocks, "base": base}
 
 
 # --------------------------------------------------------------------------
