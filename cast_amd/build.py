@@ -128,7 +128,11 @@ def build(verbose: bool = True) -> Path:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, out)
-    ext = build_torch_ops()
+    try:
+        ext = build_torch_ops()
+    except RuntimeError as e:  # the C ABI library stands; only the torch ops are missing
+        raise RuntimeError(f"{out} is built (the C ABI is usable through ctypes), but the "
+                           f"torch extension {TORCH_OPS} is not:\n{e}") from None
     if verbose:
         print(f"built {out} from {len(sources)} sources and {ext.name}")
     return out

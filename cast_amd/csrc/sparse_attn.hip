@@ -305,23 +305,23 @@ extern "C" int rcsa_sparse_attn_bf16_split(
   return launch_attn_split<false>(a, HEAD_DIM, BLOCK_M, BLOCK_N, stream);
 }
 
-extern "C" int rcsa_sparse_attn_int8_split(
-    const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
-    const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
-    const uint32_t* K_block_mask, float sm_scale, float* M, void* Out,
-    const int32_t* block_indices,
-    const int32_t* block_indices_lens, int64_t stride_qz, int64_t stride_qh,
-    int64_t stride_qm, int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
-    int64_t stride_vz, int64_t stride_vh, int64_t stride_vn, int64_t stride_oz,
-    int64_t stride_oh, int64_t stride_om, int64_t stride_bz, int64_t stride_bh,
-    int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
-    int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
-    int64_t BLOCK_N, int64_t max_k, int64_t n_split, void* workspace,
-    int64_t workspace_bytes, const int32_t* out_token, int64_t out_len, const int32_t* kv_token,
-    int64_t kv_len, hipStream_t stream) {
+// The checks and argument set-up the split int8 entry point and its
+// allocation-free variant share: everything but where the split's workspace
+// comes from.
+static int int8_setup(
+    AttnArgs& a, const int8_t* Q, const float* q_scale, int64_t q_scale_stride,
+    const int8_t* K, const float* k_scale, int64_t k_scale_stride, const void* V,
+    const uint8_t* K_valid, const uint32_t* K_block_mask, float sm_scale, float* M, void* Out,
+    const int32_t* block_indices, const int32_t* block_indices_lens, int64_t stride_qz,
+    int64_t stride_qh, int64_t stride_qm, int64_t stride_kz, int64_t stride_kh,
+    int64_t stride_kn, int64_t stride_vz, int64_t stride_vh, int64_t stride_vn,
+    int64_t stride_oz, int64_t stride_oh, int64_t stride_om, int64_t stride_bz,
+    int64_t stride_bh, int64_t stride_bm, int64_t stride_lz, int64_t stride_lh,
+    int64_t stride_lm, int64_t B, int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM,
+    int64_t BLOCK_M, int64_t BLOCK_N, int64_t max_k, const int32_t* out_token,
+    int64_t out_len, const int32_t* kv_token, int64_t kv_len) {
   if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
   if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
-  AttnArgs a{};
   a.q = Q;
   a.k = K;
   a.v = static_cast<const u16*>(V);
@@ -346,7 +346,31 @@ extern "C" int rcsa_sparse_attn_int8_split(
     a.kmask = K_block_mask;
     a.kvalid = nullptr;
   }
-  st = set_gather(a, kv_token, kv_len, BLOCK_N, false);
+  return set_gather(a, kv_token, kv_len, BLOCK_N, false);
+}
+
+extern "C" int rcsa_sparse_attn_int8_split(
+    const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
+    const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
+    const uint32_t* K_block_mask, float sm_scale, float* M, void* Out,
+    const int32_t* block_indices,
+    const int32_t* block_indices_lens, int64_t stride_qz, int64_t stride_qh,
+    int64_t stride_qm, int64_t stride_kz, int64_t stride_kh, int64_t stride_kn,
+    int64_t stride_vz, int64_t stride_vh, int64_t stride_vn, int64_t stride_oz,
+    int64_t stride_oh, int64_t stride_om, int64_t stride_bz, int64_t stride_bh,
+    int64_t stride_bm, int64_t stride_lz, int64_t stride_lh, int64_t stride_lm, int64_t B,
+    int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
+    int64_t BLOCK_N, int64_t max_k, int64_t n_split, void* workspace,
+    int64_t workspace_bytes, const int32_t* out_token, int64_t out_len, const int32_t* kv_token,
+    int64_t kv_len, hipStream_t stream) {
+  AttnArgs a{};
+  int st = int8_setup(a, Q, q_scale, q_scale_stride, K, k_scale, k_scale_stride, V, K_valid,
+                      K_block_mask, sm_scale, M, Out, block_indices, block_indices_lens,
+                      stride_qz, stride_qh, stride_qm, stride_kz, stride_kh, stride_kn,
+                      stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
+                      stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B, H,
+                      Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, out_token, out_len,
+                      kv_token, kv_len);
   if (st) return st;
   st = apply_split(a, HEAD_DIM, n_split, workspace, workspace_bytes);
   if (st) return st;
@@ -357,6 +381,8 @@ extern "C" int rcsa_sparse_attn_int8_split(
 // The split int8 entry point with the library's static scratch as its
 // workspace: allocates nothing.  Planned exactly like the split entry point;
 // a split needing more than kScratchBytes is refused with RCSA_ERR_SCRATCH.
+// Calls on one device share the scratch: the caller serialises them (one
+// stream, or an event chain between streams).
 extern "C" int rcsa_sparse_attn_int8_noalloc(
     const int8_t* Q, const float* q_scale, int64_t q_scale_stride, const int8_t* K,
     const float* k_scale, int64_t k_scale_stride, const void* V, const uint8_t* K_valid,
@@ -370,34 +396,14 @@ extern "C" int rcsa_sparse_attn_int8_noalloc(
     int64_t H, int64_t Q_LEN, int64_t K_LEN, int64_t HEAD_DIM, int64_t BLOCK_M,
     int64_t BLOCK_N, int64_t max_k, int64_t n_split, const int32_t* out_token,
     int64_t out_len, const int32_t* kv_token, int64_t kv_len, hipStream_t stream) {
-  if (!Q || !K || !V || !q_scale || !k_scale) return RCSA_ERR_NULL;
-  if (!aligned16(Q) || !aligned16(K) || !aligned16(V)) return RCSA_ERR_ALIGN;
   AttnArgs a{};
-  a.q = Q;
-  a.k = K;
-  a.v = static_cast<const u16*>(V);
-  a.q_scale = q_scale;
-  a.k_scale = k_scale;
-  a.q_scale_stride = q_scale_stride;
-  a.k_scale_stride = k_scale_stride;
-  int st = fill_common(a, K_valid, sm_scale, M, Out, block_indices, block_indices_lens,
-                       stride_qz, stride_qh, stride_qm, stride_kz, stride_kh, stride_kn,
-                       stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
-                       stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B,
-                       H, Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, 16);
-  if (st) return st;
-  if (q_scale_stride < a.n_qblocks || k_scale_stride < a.n_kblocks) return RCSA_ERR_STRIDE;
-  if (out_token) {
-    if (out_len <= 0 || out_len >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;
-    a.out_tok = out_token;
-    a.out_len = out_len;
-  }
-  if (K_block_mask) {
-    if (reinterpret_cast<uintptr_t>(K_block_mask) & 3u) return RCSA_ERR_ALIGN;
-    a.kmask = K_block_mask;
-    a.kvalid = nullptr;
-  }
-  st = set_gather(a, kv_token, kv_len, BLOCK_N, false);
+  int st = int8_setup(a, Q, q_scale, q_scale_stride, K, k_scale, k_scale_stride, V, K_valid,
+                      K_block_mask, sm_scale, M, Out, block_indices, block_indices_lens,
+                      stride_qz, stride_qh, stride_qm, stride_kz, stride_kh, stride_kn,
+                      stride_vz, stride_vh, stride_vn, stride_oz, stride_oh, stride_om,
+                      stride_bz, stride_bh, stride_bm, stride_lz, stride_lh, stride_lm, B, H,
+                      Q_LEN, K_LEN, HEAD_DIM, BLOCK_M, BLOCK_N, max_k, out_token, out_len,
+                      kv_token, kv_len);
   if (st) return st;
   st = plan_split(a, n_split);
   if (st) return st;

@@ -955,6 +955,10 @@ attn_merge_kernel(AttnArgs a) {
   const int64_t qb = item % a.n_qblocks, bh = item / a.n_qblocks;
   const int64_t qrow = qb * a.block_m + r;
   if (qrow >= a.q_len) return;
+  if (a.q_tok != nullptr) {  // a gathered query slot with no token: no share wrote it
+    const int32_t t = a.q_tok[qrow];
+    if (t < 0 || t >= a.q_src_len) return;
+  }
   const int64_t orow = out_row(a, qrow);
   if (orow < 0) return;
   float mx = -INFINITY;

@@ -152,9 +152,8 @@ class RelayLayout:
 
 def _bits32(valid: torch.Tensor, block_size: int) -> torch.Tensor:
     """bool [n * block_size] -> int32 [n, block_size // 32] (bit i of word w = slot 32 w + i)."""
-    words = valid.reshape(-1, block_size // 32, 32).to(torch.int64)
-    bits = (words << torch.arange(32, device=valid.device)).sum(-1)
-    return torch.where(bits >= 2 ** 31, bits - 2 ** 32, bits).to(torch.int32)
+    from .ops import valid_bits
+    return valid_bits(valid, block_size)
 
 
 def _slots_of(ids: torch.Tensor, members: torch.Tensor, n_rows: int, bs: int,

@@ -560,6 +560,17 @@ def _check_block_mask(block_mask, Lk, block_n, device, fn):
     return block_mask.contiguous()
 
 
+def valid_bits(valid: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Per-key validity flags ``[n_blocks * block_size]`` as the attention's
+    ``block_mask``: int32 ``[n_blocks, block_size // 32]``, bit i of word w of
+    block n = key n * block_size + 32 w + i (the form the key pooling pass writes)."""
+    if block_size % 32 or valid.numel() % block_size:
+        raise ValueError("valid_bits: block_size must be a multiple of 32 dividing the keys")
+    words = (valid.reshape(-1, block_size // 32, 32) != 0).to(torch.int64)
+    bits = (words << torch.arange(32, device=valid.device)).sum(-1)
+    return torch.where(bits >= 2 ** 31, bits - 2 ** 32, bits).to(torch.int32)
+
+
 def _bhld_strides(x: torch.Tensor, token_major: bool):
     """(stride_b, stride_h, stride_row) of [B, H, L, D] or token-major [B, L, H, D]."""
     return ((x.stride(0), x.stride(2), x.stride(1)) if token_major

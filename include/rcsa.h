@@ -425,7 +425,9 @@ int rcsa_sparse_attn_int8_split(const int8_t* Q, const float* q_scale,
  * workspace would exceed it returns RCSA_ERR_SCRATCH (n_split 3 covers up to
  * 8 * 31 = 248 tail query blocks of 128 rows at HEAD_DIM 128).  Every call on
  * one GPU shares that GPU's array: calls that overlap on one GPU (different
- * streams, or threads) race.  Arguments and results as
+ * streams, or threads) race, so the caller serialises them: one stream per
+ * device, or an event recorded after each call and waited on by the stream of
+ * the next.  Arguments and results as
  * rcsa_sparse_attn_int8_split.
  */
 int rcsa_sparse_attn_int8_noalloc(const int8_t* Q, const float* q_scale,

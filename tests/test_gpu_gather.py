@@ -153,6 +153,48 @@ def test_bf16_attention_reads_rows_through_maps(n_split):
     assert torch.equal(lse_g, lse_w[:, :, t2p])
 
 
+def test_bf16_split_leaves_empty_query_slots_unwritten():
+    """A gathered bf16 call whose output map sends empty query slots (no token)
+    to real rows: no launch form writes those rows, so the split launch equals
+    the unsplit one bit for bit, and those rows keep their previous contents."""
+    from cast_amd import ops
+    dev = torch.device("cuda:0")
+    g = torch.Generator().manual_seed(41)
+    B, H, D, nqb, nkb, max_k = 1, 24, 128, 28, 40, 12
+    nq_tok, nk_tok = nqb * 128 - 300, nkb * 128
+    q_tok = (torch.randn(B, nq_tok, H, D, generator=g) / D ** 0.5).bfloat16().to(dev)
+    k_tok = (torch.randn(B, nk_tok, H, D, generator=g) / D ** 0.5).bfloat16().to(dev)
+    v_tok = torch.randn(B, nk_tok, H, D, generator=g).bfloat16().to(dev)
+    qmap = torch.full((nqb * 128,), -1, dtype=torch.int32)
+    qslots = torch.randperm(nqb * 128, generator=g)[:nq_tok]
+    qmap[qslots] = torch.arange(nq_tok, dtype=torch.int32)
+    n_out = nq_tok + 40
+    # every slot has an output row; empty query slots write rows nq_tok.. of out
+    omap = qmap.clone()
+    empty = torch.nonzero(qmap < 0).flatten()
+    omap[empty] = nq_tok + (torch.arange(empty.numel()) % 40).int()
+    qmap, omap = qmap.to(dev), omap.to(dev)
+    kmap = torch.arange(nk_tok, dtype=torch.int32, device=dev)
+    mask = torch.full((nkb, 4), -1, dtype=torch.int32, device=dev)
+    idx = torch.stack([torch.randperm(nkb, generator=g)[:max_k].sort().values
+                       for _ in range(B * H * nqb)]).reshape(B, H, nqb, max_k).int().to(dev)
+    cnt = torch.randint(1, max_k + 1, (B, H, nqb), generator=g, dtype=torch.int32).to(dev)
+    outs = []
+    for ns in (1, 3):
+        out = torch.full((B, n_out, H, D), 7.0, dtype=torch.bfloat16, device=dev)
+        print(f"bf16 empty query slots, n_split {ns}", flush=True)
+        ops.sparse_attn_bf16(q_tok, k_tok, v_tok, idx, cnt, None, block_mask=mask,
+                             n_split=ns, q_token=qmap, kv_token=kmap, out_token=omap,
+                             out_len=n_out, out=out)
+        outs.append(out)
+    torch.cuda.synchronize()
+    for out in outs:
+        assert bool((out[:, nq_tok:] == 7.0).all())
+    # the merge sums the shares' partials in another order than one pass does
+    torch.testing.assert_close(outs[1][:, :nq_tok].float(), outs[0][:, :nq_tok].float(),
+                               atol=2e-3, rtol=1e-2)
+
+
 @pytest.mark.parametrize("int8", [True, False])
 @pytest.mark.parametrize("n_split", [1, 3])
 def test_gathered_layer_call_matches_pack_unpack(n_split, int8):

@@ -218,3 +218,22 @@ def test_transport_operator_matches_oracle():
     assert torch.equal(fc_transport_operator(tr, (0, 6), (6, 5), 0.0), torch.eye(30))
     assert fc_transport_operator(tr, (1, 6), (6, 5), 0.5) is None
     assert fc_transport_operator(None, (0, 6), (6, 5), 0.5) is None
+
+
+def test_valid_bits_layout():
+    """Key validity flags as the attention's block_mask words: bit i of word w
+    of block n is key n * block_size + 32 w + i (a pure-Python loop)."""
+    from cast_amd.ops import valid_bits
+    g = torch.Generator().manual_seed(3)
+    for bs in (64, 128):
+        valid = torch.rand(5 * bs, generator=g) > 0.3
+        got = valid_bits(valid, bs)
+        assert got.shape == (5, bs // 32) and got.dtype == torch.int32
+        for n in range(5):
+            for w in range(bs // 32):
+                word = 0
+                for i in range(32):
+                    word |= int(valid[n * bs + 32 * w + i]) << i
+                assert (int(got[n, w]) & 0xffffffff) == word
+    with pytest.raises(ValueError):
+        valid_bits(torch.ones(100, dtype=torch.bool), 64)
