@@ -8,12 +8,15 @@
 // acc = sum_k x[m][k] w[n][k] in int32.  A workgroup (8 wavefronts, one per CU)
 // computes a 256 (tokens) x 256 (channels) tile; each wavefront 64 x 128 as
 // 2 x 4 tiles of v_mfma_i32_32x32x32_i8 with the weights as the A operand, so a
-// lane ends up holding one token and runs of 4 consecutive channels (8-byte
-// stores).  Both operands are staged by direct-to-LDS copies through a 3-slot
-// ring of 64-byte K steps (32 KiB per slot); 16-byte chunks of each 64-byte row
-// are XORed by (row / 4) mod 4 so the ds_read_b128 operand reads are conflict
-// free.  When the 256 x 256 tiles would end in a short round, the rows of that
-// round run as 128 x 128 tiles (each wavefront 32 x 64) of the same launch.
+// lane ends up holding one token and runs of 4 consecutive channels; lanes l and
+// l + 32 swap halves (v_permlane32_swap) so that each stores 8 consecutive
+// channels (16 bytes).  Both operands are staged by direct-to-LDS copies through
+// a 2-slot ring of 128-byte K steps (64 KiB per slot), so every row a copy reads
+// is one whole 128-byte line (half as many L2 requests as 64-byte steps);
+// 16-byte chunks of each 128-byte row are XORed by (row / 2) mod 8 so the
+// ds_read_b128 operand reads are conflict free.  When the 256 x 256 tiles would
+// end in a short round, the rows of that round run as 128 x 128 tiles (each
+// wavefront 32 x 64) of the same launch.
 #include <type_traits>
 
 #include "rcsa_common.h"
@@ -24,7 +27,7 @@ namespace rcsa {
 
 constexpr int kQThreads = 256;       // quantiser: 4 rows per workgroup
 constexpr int kGemmThreads = 512;    // 8 wavefronts: 4 (tokens) x 2 (channels)
-constexpr int kKS = 64;              // bytes of K per ring step
+constexpr int kKS = 128;             // bytes of K per ring step (one 128-byte line per row)
 
 template <typename T>
 __device__ __forceinline__ float to_f32(T v) {
@@ -85,8 +88,8 @@ __device__ __forceinline__ void dma16(const int8_t* base, int bytes, uint32_t vo
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, RCSA_QKV_LDS(void, dst), 16, voff, soff, 0, 0);
 }
 
-// chunk XOR of a 64-byte row: (row / 4) mod 4
-__device__ __forceinline__ int qkv_swz(int row) { return (row >> 2) & 3; }
+// chunk XOR of a 128-byte row: (row / 2) mod 8
+__device__ __forceinline__ int qkv_swz(int row) { return (row >> 1) & 7; }
 
 // s_waitcnt immediate for vmcnt <= n only (gfx9 encoding)
 constexpr int qkv_vmcnt(int n) {
@@ -105,22 +108,23 @@ template <int TMT, int TNT>
 struct LinTile {
   static constexpr int BM = 4 * 32 * TMT, BN = 2 * 32 * TNT;
   static constexpr int XB = BM * kKS, WB = BN * kKS;          // bytes of a ring step
-  static constexpr int XU = BM / 16 / 8, WU = BN / 16 / 8;    // 1 KiB copy units per wavefront
+  static constexpr int XU = XB / 1024 / 8, WU = WB / 1024 / 8;  // 1 KiB copy units per wavefront
   static constexpr int OPS = XU + WU;                         // copies per wavefront and step
+  static constexpr int KS = kKS / 32;                         // MFMA k-steps per ring step
   static_assert(XU == WU && XU >= 1, "both tiles are copied by the same rows");
 };
 
 template <int TMT, int TNT>
 __device__ __forceinline__ void linear_tile(const LinearArgs& a, int64_t m0, int64_t n0,
-                                            char* s_0, char* s_1, char* s_2) {
+                                            char* s_0, char* s_1) {
   using T = LinTile<TMT, TNT>;
   const int t = threadIdx.x, lane = t % kWave;
   const int wave = __builtin_amdgcn_readfirstlane(t / kWave);
   const int wm = wave & 3, wn = wave >> 2;
 
-  // copies: each tile is units of 1 KiB (16 rows each); a wavefront copies
-  // XU + WU units per ring step.  Lane l lands at row 16 u + l / 4, chunk l % 4
-  // of its unit and loads the chunk that the swizzle puts there.
+  // copies: each tile is units of 1 KiB (8 rows of 128 bytes); a wavefront
+  // copies XU + WU units per ring step.  Lane l lands at row 8 u + l / 8, chunk
+  // l % 8 of its unit and loads the chunk that the swizzle puts there.
   const int64_t rows_x = a.M - m0 < T::BM ? a.M - m0 : T::BM;
   const int8_t* xb = a.x + m0 * a.K;
   const int8_t* wb = a.w + n0 * a.K;
@@ -128,8 +132,8 @@ __device__ __forceinline__ void linear_tile(const LinearArgs& a, int64_t m0, int
   uint32_t off[T::XU];  // the same rows of both tiles
 #pragma unroll
   for (int i = 0; i < T::XU; ++i) {
-    const int r = (wave * T::XU + i) * 16 + lane / 4;
-    off[i] = static_cast<uint32_t>(r * a.K + ((lane & 3) ^ qkv_swz(r)) * 16);
+    const int r = (wave * T::XU + i) * 8 + lane / 8;
+    off[i] = static_cast<uint32_t>(r * a.K + ((lane & 7) ^ qkv_swz(r)) * 16);
   }
   const int steps = static_cast<int>(a.K / kKS);
   auto stage = [&](int s, char* dst) __attribute__((always_inline)) {
@@ -146,18 +150,18 @@ __device__ __forceinline__ void linear_tile(const LinearArgs& a, int64_t m0, int
 
   // operand read offsets: row r of a tile, chunk c = 2 ks + lane half
   const int hf = lane >> 5, li = lane & 31;
-  int xo[TMT][2], wo[TNT][2];
+  int xo[TMT][T::KS], wo[TNT][T::KS];
 #pragma unroll
   for (int tmi = 0; tmi < TMT; ++tmi)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < T::KS; ++ks) {
       const int r = wm * 32 * TMT + tmi * 32 + li;
       xo[tmi][ks] = r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
     }
 #pragma unroll
   for (int tni = 0; tni < TNT; ++tni)
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < T::KS; ++ks) {
       const int r = wn * 32 * TNT + tni * 32 + li;
       wo[tni][ks] = T::XB + r * kKS + (((ks * 2 + hf) ^ qkv_swz(r)) * 16);
     }
@@ -171,51 +175,51 @@ __device__ __forceinline__ void linear_tile(const LinearArgs& a, int64_t m0, int
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0;
 
   stage(0, s_0);
-  __builtin_amdgcn_sched_barrier(0);  // step 0's copies stay older than step 1's
-  stage(1, s_1);
   auto compute = [&](const char* tile, int s_fill, char* fill) __attribute__((always_inline)) {
-    v4i xf[2][TMT], wf[2][TNT];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int i = 0; i < TMT; ++i) xf[ks][i] = *reinterpret_cast<const v4i*>(tile + xo[i][ks]);
-#pragma unroll
-      for (int i = 0; i < TNT; ++i) wf[ks][i] = *reinterpret_cast<const v4i*>(tile + wo[i][ks]);
-    }
     stage(s_fill, fill);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < T::KS; ++ks) {
+      v4i xf[TMT], wf[TNT];
+#pragma unroll
+      for (int i = 0; i < TMT; ++i) xf[i] = *reinterpret_cast<const v4i*>(tile + xo[i][ks]);
+#pragma unroll
+      for (int i = 0; i < TNT; ++i) wf[i] = *reinterpret_cast<const v4i*>(tile + wo[i][ks]);
 #pragma unroll
       for (int tni = 0; tni < TNT; ++tni)
 #pragma unroll
         for (int tmi = 0; tmi < TMT; ++tmi)
-          acc[tni][tmi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[ks][tni], xf[ks][tmi],
-                                                                acc[tni][tmi], 0, 0, 0);
-    // the ks = 0 operands first, then each MFMA with one ks = 1 read or one copy
-    constexpr int kReads = TMT + TNT;
+          acc[tni][tmi] = __builtin_amdgcn_mfma_i32_32x32x32_i8(wf[tni], xf[tmi], acc[tni][tmi],
+                                                                0, 0, 0);
+    }
+    // the copies of the next step first, then the k-step 0 operands, then each
+    // MFMA with one operand read of the following k-steps
+    constexpr int kReads = TMT + TNT, kMfma = TMT * TNT;
+    __builtin_amdgcn_sched_group_barrier(0x020, T::OPS, 0);
     __builtin_amdgcn_sched_group_barrier(0x100, kReads, 0);
 #pragma unroll
-    for (int i = 0; i < 2 * TMT * TNT; ++i) {
+    for (int i = 0; i < T::KS * kMfma; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      if (i < kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      if (i >= kReads && i < kReads + T::OPS) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+      if (i < (T::KS - 1) * kReads) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
     }
   };
-  // ring: step j lives in slot j % 3; the copies of step j + 2 go out while
-  // step j is computed, so every wavefront has OPS copies per step in flight
-  // (the host keeps the step count a multiple of 3)
-  for (int j = 0; j < steps; j += 3) {
-    qkv_wait_barrier<T::OPS>();
-    compute(s_0, j + 2, s_2);
-    qkv_wait_barrier<T::OPS>();
-    compute(s_1, j + 3, s_0);
-    qkv_wait_barrier<T::OPS>();
-    compute(s_2, j + 4, s_1);
+  // ring of two slots: step j lives in slot j % 2; the copies of step j + 1
+  // go out at the start of step j, after every wavefront has finished step
+  // j - 1 and step j has landed
+  for (int j = 0; j + 1 < steps; j += 2) {
+    qkv_wait_barrier<0>();
+    compute(s_0, j + 1, s_1);
+    qkv_wait_barrier<0>();
+    compute(s_1, j + 2, s_0);
+  }
+  if (steps & 1) {  // the last step of an odd count, in slot 0; its copies are empty
+    qkv_wait_barrier<0>();
+    compute(s_0, steps, s_1);
   }
   __builtin_amdgcn_s_waitcnt(qkv_vmcnt(0));
 
   // epilogue: lane holds token m = li of each 32-token tile and channels
-  // 8 g + 4 hf + (0..3) of each 32-channel tile
+  // 8 g + 4 hf + (0..3) of each 32-channel tile; lanes l and l + 32 swap
+  // halves so that each stores 8 consecutive channels (16 bytes)
 #pragma unroll
   for (int tmi = 0; tmi < TMT; ++tmi) {
     const int64_t m = m0 + wm * 32 * TMT + tmi * 32 + li;
@@ -225,22 +229,38 @@ __device__ __forceinline__ void linear_tile(const LinearArgs& a, int64_t m0, int
 #pragma unroll
     for (int tni = 0; tni < TNT; ++tni)
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int64_t n = n0 + wn * 32 * TNT + tni * 32 + 8 * g + 4 * hf;
-        const float4 ws = *reinterpret_cast<const float4*>(a.ws + n);
-        float y[4] = {static_cast<float>(acc[tni][tmi][4 * g + 0]) * xs * ws.x,
-                      static_cast<float>(acc[tni][tmi][4 * g + 1]) * xs * ws.y,
-                      static_cast<float>(acc[tni][tmi][4 * g + 2]) * xs * ws.z,
-                      static_cast<float>(acc[tni][tmi][4 * g + 3]) * xs * ws.w};
-        if (a.bias != nullptr) {
-          const uint2 bb = *reinterpret_cast<const uint2*>(a.bias + n);
-          const float bv[4] = {__uint_as_float(bb.x << 16), __uint_as_float(bb.x & 0xffff0000u),
-                               __uint_as_float(bb.y << 16), __uint_as_float(bb.y & 0xffff0000u)};
+      for (int p = 0; p < 2; ++p) {
+        uint32_t pk[2][2];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) y[e] = bf16_to_f32(f32_to_bf16(y[e])) + bv[e];
+        for (int gg = 0; gg < 2; ++gg) {
+          const int g = 2 * p + gg;
+          const int64_t n = n0 + wn * 32 * TNT + tni * 32 + 8 * g + 4 * hf;
+          const float4 ws = *reinterpret_cast<const float4*>(a.ws + n);
+          float y[4] = {static_cast<float>(acc[tni][tmi][4 * g + 0]) * xs * ws.x,
+                        static_cast<float>(acc[tni][tmi][4 * g + 1]) * xs * ws.y,
+                        static_cast<float>(acc[tni][tmi][4 * g + 2]) * xs * ws.z,
+                        static_cast<float>(acc[tni][tmi][4 * g + 3]) * xs * ws.w};
+          if (a.bias != nullptr) {
+            const uint2 bb = *reinterpret_cast<const uint2*>(a.bias + n);
+            const float bv[4] = {__uint_as_float(bb.x << 16), __uint_as_float(bb.x & 0xffff0000u),
+                                 __uint_as_float(bb.y << 16), __uint_as_float(bb.y & 0xffff0000u)};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) y[e] = bf16_to_f32(f32_to_bf16(y[e])) + bv[e];
+          }
+          pk[gg][0] = pack_bf16x2(y[0], y[1]);
+          pk[gg][1] = pack_bf16x2(y[2], y[3]);
         }
-        *reinterpret_cast<uint2*>(orow + n) =
-            make_uint2(pack_bf16x2(y[0], y[1]), pack_bf16x2(y[2], y[3]));
+        // lane l (half 0) keeps channels 8(2p) + 0..3 and takes + 4..7 from
+        // lane l + 32, which keeps 8(2p + 1) + 4..7 and takes + 0..3
+        uint32_t st[4];
+#pragma unroll
+        for (int w = 0; w < 2; ++w) {
+          const auto r = __builtin_amdgcn_permlane32_swap(pk[0][w], pk[1][w], false, false);
+          st[w] = r[0];
+          st[2 + w] = r[1];
+        }
+        const int64_t n = n0 + wn * 32 * TNT + tni * 32 + 8 * (2 * p + hf);
+        *reinterpret_cast<uint4*>(orow + n) = make_uint4(st[0], st[1], st[2], st[3]);
       }
   }
 }
@@ -252,7 +272,6 @@ __global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_
 int8_linear_kernel(LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char s_0[BigTile::XB + BigTile::WB];
   __shared__ __attribute__((aligned(1024))) char s_1[BigTile::XB + BigTile::WB];
-  __shared__ __attribute__((aligned(1024))) char s_2[BigTile::XB + BigTile::WB];
   if (static_cast<int64_t>(blockIdx.x) < a.big_grid) {
     // XCD-aware order in groups of kGroupM token blocks: consecutive tiles of
     // one XCD walk the group's token blocks for one channel block, then the
@@ -267,7 +286,7 @@ int8_linear_kernel(LinearArgs a) {
     const int64_t group = tile / (kGroupM * tiles_n), in_group = tile % (kGroupM * tiles_n);
     const int64_t group_m = n_m - group * kGroupM < kGroupM ? n_m - group * kGroupM : kGroupM;
     const int64_t tm = group * kGroupM + in_group % group_m, tn = in_group / group_m;
-    linear_tile<2, 4>(a, tm * BigTile::BM, tn * BigTile::BN, s_0, s_1, s_2);
+    linear_tile<2, 4>(a, tm * BigTile::BM, tn * BigTile::BN, s_0, s_1);
   } else {
     // the rows after big_rows in 128 x 128 tiles: they fill the last round,
     // which whole 256 x 256 tiles would leave mostly idle
@@ -276,7 +295,7 @@ int8_linear_kernel(LinearArgs a) {
     const int64_t tile = xcd_remap(blockIdx.x - a.big_grid, n_m * tiles_n);
     if (tile < 0) return;
     const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
-    linear_tile<1, 2>(a, a.big_rows + tm * SmallTile::BM, tn * SmallTile::BN, s_0, s_1, s_2);
+    linear_tile<1, 2>(a, a.big_rows + tm * SmallTile::BM, tn * SmallTile::BN, s_0, s_1);
   }
 }
 
@@ -307,7 +326,7 @@ extern "C" int rcsa_int8_linear(const int8_t* x, const float* x_scale, const int
                                 const float* w_scale, const void* bias, int64_t M, int64_t N,
                                 int64_t K, void* out, int64_t ldo, hipStream_t stream) {
   if (!x || !x_scale || !w || !w_scale || !out) return RCSA_ERR_NULL;
-  if (M <= 0 || N <= 0 || K <= 0 || N % BigTile::BN || K % (3 * kKS) || ldo < N || ldo % 4)
+  if (M <= 0 || N <= 0 || K <= 0 || N % BigTile::BN || K % kKS || ldo < N || ldo % 4)
     return RCSA_ERR_SHAPE;
   // the copies address a tile with 32-bit offsets
   if (static_cast<int64_t>(BigTile::BM) * K >= (int64_t{1} << 31)) return RCSA_ERR_SHAPE;

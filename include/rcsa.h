@@ -591,7 +591,7 @@ int rcsa_route_check(const int32_t* base, const int32_t* selected, const int32_t
  * + bias[n]), acc = sum_k x[m][k] w[n][k] (int32), for x int8 [M][K], w int8
  * [N][K] (both 16-byte aligned), w_scale fp32 [N] (16-byte aligned), bias bf16
  * [N] or NULL (then out = bf16(float(acc) * x_scale * w_scale)); out bf16 with
- * row stride ldo (8-byte aligned).  N a multiple of 256, K a multiple of 192.
+ * row stride ldo (8-byte aligned).  N a multiple of 256, K a multiple of 128.
  */
 int rcsa_quantize_rows_int8(const void* x, int dtype, int64_t M, int64_t C, int64_t ldx,
                             int8_t* q, float* scale, hipStream_t stream);

@@ -45,19 +45,19 @@ def test_int8_linear_matches_oracle(dev, M, with_bias):
 
 
 def test_int8_linear_short_last_round(dev):
-    """5800 x 3072 x 192: 23 row blocks x 12 channel blocks of 256 x 256 tiles
+    """5800 x 3072 x 128: 23 row blocks x 12 channel blocks of 256 x 256 tiles
     leave a short last round on 256 compute units, so the last 424 rows run as
     128 x 128 tiles (the last one 40 rows); every output element against the
     oracle, bit for bit."""
     from cast_amd import ops
     g = torch.Generator().manual_seed(11)
-    M, N, K = 5800, 3072, 192
+    M, N, K = 5800, 3072, 128
     x = torch.randint(-127, 128, (M, K), generator=g, dtype=torch.int8)
     w = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int8)
     xs = torch.rand(M, generator=g) * 0.01 + 1e-4
     ws = torch.rand(N, generator=g) * 0.01 + 1e-4
     bias = torch.randn(N, generator=g).bfloat16()
-    print("int8 linear 5800 x 3072 x 192", flush=True)
+    print("int8 linear 5800 x 3072 x 128", flush=True)
     got = ops.int8_linear(x.to(dev), xs.to(dev), w.to(dev), ws.to(dev), bias.to(dev))
     torch.cuda.synchronize()
     assert torch.equal(got.cpu(), orc.int8_linear(x, xs, w, ws, bias))
@@ -95,7 +95,7 @@ def test_shared_qkv_matrix_shape(dev):
 def test_forward_coordinator_order(dev):
     from cast_amd.qkv import SharedInt8QKVForwardCoordinator, shared_int8_qkv
     g = torch.Generator().manual_seed(4)
-    C = 768  # channels a multiple of 256, the input width a multiple of 192
+    C = 768  # channels a multiple of 256, the input width a multiple of 128
     mods = [_int8_module(g, C, C, dev) for _ in range(3)]
     for m in mods:
         m.forward = lambda x: None
