@@ -16,7 +16,7 @@
 // 16-byte chunks of each 128-byte row are XORed by (row / 2) mod 8 so the
 // ds_read_b128 operand reads are conflict free.  When the 256 x 256 tiles would
 // end in a short round, the rows of that round run as 128 x 128 tiles (each
-// wavefront 32 x 64) of the same launch.
+// wavefront 32 x 64) of the same launch, dispatched first.
 #include <type_traits>
 
 #include "rcsa_common.h"
@@ -74,8 +74,9 @@ struct LinearArgs {
   const u16* bias;      // [N] bf16 or NULL
   u16* out;             // [M, ldo] bf16
   int64_t M, N, K, ldo;
-  // one launch: 256 x 256 tiles over rows [0, big_rows) on the first big_grid
-  // workgroups, then 128 x 128 tiles over rows [big_rows, M)
+  // one launch: 128 x 128 tiles over rows [big_rows, M) on the first
+  // gridDim.x - big_grid workgroups, then 256 x 256 tiles over rows [0, big_rows)
+  // on the last big_grid
   int64_t big_rows, big_grid;
 };
 
@@ -272,7 +273,15 @@ __global__ void __launch_bounds__(kGemmThreads) __attribute__((amdgpu_waves_per_
 int8_linear_kernel(LinearArgs a) {
   __shared__ __attribute__((aligned(1024))) char s_0[BigTile::XB + BigTile::WB];
   __shared__ __attribute__((aligned(1024))) char s_1[BigTile::XB + BigTile::WB];
-  if (static_cast<int64_t>(blockIdx.x) < a.big_grid) {
+  // the 128 x 128 tiles take the first workgroup slots: the compute units that
+  // run one start their 256 x 256 tiles a quarter tile later than the others,
+  // so the two groups' output stores fall beside the other group's MFMAs
+  // instead of all at once (0.417 against 0.428 ms at 38,720 x 3072 x 3072)
+  const int64_t small_grid = static_cast<int64_t>(gridDim.x) - a.big_grid;
+  const int64_t bid = static_cast<int64_t>(blockIdx.x) >= small_grid
+                          ? static_cast<int64_t>(blockIdx.x) - small_grid
+                          : static_cast<int64_t>(blockIdx.x) + a.big_grid;
+  if (bid < a.big_grid) {
     // XCD-aware order in groups of kGroupM token blocks: consecutive tiles of
     // one XCD walk the group's token blocks for one channel block, then the
     // next channel block, so the 32 workgroups resident on an XCD at once share
@@ -281,18 +290,18 @@ int8_linear_kernel(LinearArgs a) {
     constexpr int64_t kGroupM = 4;
     const int64_t n_m = (a.big_rows + BigTile::BM - 1) / BigTile::BM;
     const int64_t tiles_n = a.N / BigTile::BN;
-    const int64_t tile = xcd_remap(blockIdx.x, n_m * tiles_n);
+    const int64_t tile = xcd_remap(bid, n_m * tiles_n);
     if (tile < 0) return;
     const int64_t group = tile / (kGroupM * tiles_n), in_group = tile % (kGroupM * tiles_n);
     const int64_t group_m = n_m - group * kGroupM < kGroupM ? n_m - group * kGroupM : kGroupM;
     const int64_t tm = group * kGroupM + in_group % group_m, tn = in_group / group_m;
     linear_tile<2, 4>(a, tm * BigTile::BM, tn * BigTile::BN, s_0, s_1);
   } else {
-    // the rows after big_rows in 128 x 128 tiles: they fill the last round,
-    // which whole 256 x 256 tiles would leave mostly idle
+    // the rows after big_rows in 128 x 128 tiles: the work of a short last
+    // round, which whole 256 x 256 tiles would leave mostly idle
     const int64_t n_m = (a.M - a.big_rows + SmallTile::BM - 1) / SmallTile::BM;
     const int64_t tiles_n = a.N / SmallTile::BN;
-    const int64_t tile = xcd_remap(blockIdx.x - a.big_grid, n_m * tiles_n);
+    const int64_t tile = xcd_remap(bid - a.big_grid, n_m * tiles_n);
     if (tile < 0) return;
     const int64_t tm = tile / tiles_n, tn = tile % tiles_n;
     linear_tile<1, 2>(a, a.big_rows + tm * SmallTile::BM, tn * SmallTile::BN, s_0, s_1);
@@ -336,7 +345,8 @@ extern "C" int rcsa_int8_linear(const int8_t* x, const float* x_scale, const int
     return RCSA_ERR_ALIGN;
   // 256 x 256 tiles, except that a short last round (fewer tiles than half the
   // compute units) is re-cut: the rows its tiles would cover go to 128 x 128
-  // tiles, a quarter of the work each, dispatched last to fill that round
+  // tiles, a quarter of the work each, dispatched first (which also offsets
+  // the rounds of the compute units that take one)
   const int64_t big_n = N / BigTile::BN;
   const int64_t all_big = ((M + BigTile::BM - 1) / BigTile::BM) * big_n;
   int64_t big_rows = M;
