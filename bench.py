@@ -293,11 +293,13 @@ def main() -> int:
                     help="issue each timed layer call as one HIP graph replay (default) "
                          "or as the eager Python call")
     ap.add_argument("--only", choices=["attn_int8", "attn_bf16", "copy", "layer", "compact",
-                                       "compact_bf16", "router", "qkv"],
+                                       "compact_bf16", "router", "qkv", "sweep"],
                     default=None,
                     help="profiling mode: run only this kernel (or the whole int8 layer "
                          "call, or the gathered call on the Matrix latent grid) --steps "
-                         "times after --warmup, and print its average time")
+                         "times after --warmup, and print its average time; 'sweep' runs "
+                         "--steps int8 attention launches per layer of the 30-layer step "
+                         "sweep, in layer order")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU (the RCSA path needs no collective; "
@@ -337,6 +339,29 @@ def main() -> int:
     w = workloads.matrix_dit(args.seed, int8=args.only != "attn_bf16").to(dev)
     bs = w.block_size
     max_k = w.k_total
+
+    if args.only == "sweep":
+        # the 30-layer step sweep's attention launches for per-layer counters:
+        # every layer's selection first (one layer call each), then --steps int8
+        # attention launches per layer in layer order, one JSON line per layer
+        plan = workloads.step_sweep_plan(args.seed)
+        layers = [workloads.step_layer_view(w, p) for p in plan]
+        prepared = []
+        for lw in layers:
+            r = rcsa_attention(lw.q, lw.k, lw.v, lw.q_valid, lw.k_valid, block_size=bs,
+                               k_select=lw.k_total, forced=lw.forced, int8=True,
+                               max_k=lw.k_total)
+            prepared.append((lw, r, torch.empty_like(lw.q)))
+        torch.cuda.synchronize()
+        for i, ((lw, r, o), p) in enumerate(zip(prepared, plan)):
+            for _ in range(args.steps):
+                ops.sparse_attn_int8(r.q_i8, r.q_scale, r.k_i8, r.k_scale, lw.v, r.indices,
+                                     r.counts, None, out=o, block_mask=r.k_mask)
+            torch.cuda.synchronize()
+            print(json.dumps({"only": "sweep", "layer": i, "query_frames": p["query_frames"],
+                              "fraction": p["fraction"], "launches": args.steps,
+                              "ops": lw.attention_ops(r.indices, r.counts)}), flush=True)
+        return 0
 
     if args.only == "layer":
         def layer():
