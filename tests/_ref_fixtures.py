@@ -1,8 +1,11 @@
-"""Loading of the reference-produced router and closed-loop fixtures
-(tests/golden/ref_router.npz, ref_closed_loop.npz; written by
+"""Loading of the reference-produced router, closed-loop and select fixtures
+(tests/golden/ref_router.npz, ref_closed_loop.npz, ref_select.npz; written by
 tests/golden/make_ref_golden.py) into the oracle's and the product's argument
-forms.  Shared by the CPU and GPU fixture tests."""
+forms.  Shared by the CPU and GPU fixture tests (and by the script, for the
+select cases' seeded inputs)."""
 import functools
+import math
+import random
 
 import numpy as np
 import torch
@@ -133,3 +136,66 @@ def closed_loop_case(ci: int) -> dict:
             "curvature_stats": [float(v) for v in fx[pre + "curvature_stats"]],
             "normalized": curvature / curvature.mean(dim=0, keepdim=True).clamp_min(eps),
             "time_cells": _t(fx[pre + "time_cells"])}
+
+
+# ---- the native layers' select() (P/qk_uncertainty_tangent_attention.py:988-1082) ----
+# (seed, batch, heads, head_dim, frames, latent height, latent width, tile, degree)
+SELECT_CASES = [
+    dict(seed=400, B=1, H=2, D=64, T=8, height=6, width=10, block_shape=(4, 4, 4), degree=7),
+    dict(seed=401, B=1, H=2, D=128, T=8, height=22, width=40, block_shape=(4, 4, 8),
+         degree=15),
+    dict(seed=402, B=2, H=1, D=64, T=10, height=8, width=16, block_shape=(4, 4, 8), degree=6),
+]
+
+
+def select_grid(case: dict):
+    tt, th, tw = case["block_shape"]
+    cells = math.ceil(case["T"] / tt)
+    nh, nw = math.ceil(case["height"] / th), math.ceil(case["width"] / tw)
+    return cells, nh, nw
+
+
+def select_inputs(case: dict):
+    """fp32 q, k [B, H, T*height*width, D]: N(0, 1)/sqrt(D) plus a per-frame
+    N(0, 0.3) mean shift; and their fingerprint (sum, |sum| of each)."""
+    g = torch.Generator().manual_seed(case["seed"])
+    B, H, D, T = case["B"], case["H"], case["D"], case["T"]
+    L = T * case["height"] * case["width"]
+    out = []
+    for _ in range(2):
+        x = torch.randn(B, H, T, L // T, D, generator=g) / math.sqrt(D)
+        x = x + torch.randn(B, H, T, 1, D, generator=g) * 0.3
+        out.append(x.reshape(B, H, L, D).contiguous())
+    q, k = out
+    fp = [float(q.double().sum()), float(q.double().abs().sum()),
+          float(k.double().sum()), float(k.double().abs().sum())]
+    return q, k, fp
+
+
+def select_budgets(case: dict):
+    """(blocks, degree, per-row budgets): the fixed degree moved between rows,
+    every row keeping at least its local stencil and at most every block."""
+    cells, nh, nw = select_grid(case)
+    nb = cells * nh * nw
+    local_max = 1 + sum(min(2, n - 1) for n in (cells, nh, nw))
+    degree = case["degree"]
+    rows = [degree] * nb
+    rng = random.Random(case["seed"])
+    for _ in range(nb):
+        a, b, t = rng.randrange(nb), rng.randrange(nb), rng.randint(1, 2)
+        if a != b and rows[a] - t >= local_max and rows[b] + t <= nb:
+            rows[a] -= t
+            rows[b] += t
+    return nb, degree, rows
+
+
+def select_case(ci: int) -> dict:
+    fx = router_fixture("select")
+    pre = f"select{ci}_"
+    case = SELECT_CASES[ci]
+    q, k, fp = select_inputs(case)
+    if not np.allclose(np.array(fp), fx[pre + "fingerprint"], rtol=1e-12, atol=1e-9):
+        raise RuntimeError(f"select case {ci}: seeded inputs drifted from the fixture")
+    return {"case": case, "q": q, "k": k, "rows": fx[pre + "rows"].tolist(),
+            "selected": _t(fx[pre + "selected"]), "counts": _t(fx[pre + "counts"]),
+            "report": fx[pre + "report"].tolist()}

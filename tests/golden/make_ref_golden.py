@@ -26,9 +26,19 @@ seeded CPU inputs, what these functions return:
   curvature that saturates rows.  The method runs on an instance whose
   attributes are set directly (the fields it reads), not through compile().
 
+* ``MatrixTrajectoryAdaptiveBudgetAttentionCompiler.select``
+  (P/qk_uncertainty_tangent_attention.py:988-1082): the native layers'
+  selection (visual tiling, pooled cosine scores, the +1e6 local stencil,
+  the stable descending argsort cut at each row's budget) on three seeded
+  cases with non-uniform row budgets (``tests/golden/ref_select.npz``).  The
+  inputs are regenerated from their seeds (``select_inputs``, also used by
+  the tests) and fingerprinted.
+
 Fixtures hold inputs and outputs only (numpy arrays, no pickles); the tests
 feed the inputs to the oracle and the product and compare with the outputs.
 P/ = src/interaction_accel/methods/proposed/.
+
+    python tests/golden/make_ref_golden.py [/path/to/CAST] [router|closed_loop|select ...]
 """
 from __future__ import annotations
 
@@ -40,11 +50,16 @@ import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-REF = sys.argv[1] if len(sys.argv) > 1 else "/root/reference"
+_ARGS = [a for a in sys.argv[1:] if a not in ("router", "closed_loop", "select")]
+ONLY = [a for a in sys.argv[1:] if a in ("router", "closed_loop", "select")]
+REF = _ARGS[0] if _ARGS else "/root/reference"
 sys.path.insert(0, os.path.join(REF, "src"))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
 
 from interaction_accel.methods.proposed import fc_pasm_swap_routing as R  # noqa: E402
 from interaction_accel.methods.proposed import control_response_cwca_attention as C  # noqa: E402
+from interaction_accel.methods.proposed import qk_uncertainty_tangent_attention as Q  # noqa: E402
+from tests._ref_fixtures import SELECT_CASES, select_budgets, select_inputs  # noqa: E402
 
 Router = R.FCPASMLocalCoordinateSwapRouter
 
@@ -272,17 +287,58 @@ def closed_loop_cases(fx):
                                         target_per_worldline=18).numpy()
 
 
+def select_cases(fx):
+    """The reference's own select() on a bare compiler instance holding the
+    attributes it reads (budgets as set_layer_index would install them)."""
+    TABA = Q.MatrixTrajectoryAdaptiveBudgetAttentionCompiler
+    for ci, case in enumerate(SELECT_CASES):
+        q, k, fp = select_inputs(case)
+        nb, degree, rows = select_budgets(case)
+        comp = TABA.__new__(TABA)
+        comp._block_shape = tuple(case["block_shape"])
+        comp._num_blocks = nb
+        comp._degree = degree
+        comp._row_degrees = torch.tensor(rows, dtype=torch.long)
+        comp._ray_motion = torch.linspace(0.1, 1.0, nb)
+        comp._first_order_motion = torch.linspace(0.2, 0.8, nb)
+        comp.trajectory_complexity_kind = "motion_magnitude"
+        B, H = q.shape[:2]
+        counts_in = torch.full((B, H, nb), degree, dtype=torch.int32)
+        sel, counts, rep = comp.select(
+            q, k, geometry_indices=torch.zeros(B, H, nb, degree, dtype=torch.int32),
+            geometry_counts=counts_in, latent_hw=(case["height"], case["width"]),
+            block_shape=tuple(case["block_shape"]))
+        pre = f"select{ci}_"
+        fx[pre + "fingerprint"] = np.array(fp, dtype=np.float64)
+        fx[pre + "rows"] = np.array(rows, dtype=np.int64)
+        fx[pre + "selected"] = sel.numpy()
+        fx[pre + "counts"] = counts.numpy()
+        fx[pre + "report"] = np.array([rep.mean_selected_qk_cosine, rep.protected_local_edges,
+                                       rep.missing_local_edges, rep.budget_min, rep.budget_max,
+                                       rep.budget_total], dtype=np.float64)
+
+
 def main():
     torch.manual_seed(0)
-    fx = {}
-    transport_cases(fx)
-    objective_cases(fx)
-    refine_cases(fx)
-    np.savez_compressed(os.path.join(HERE, "ref_router.npz"), **fx)
-    fc = {}
-    closed_loop_cases(fc)
-    np.savez_compressed(os.path.join(HERE, "ref_closed_loop.npz"), **fc)
-    for name, d in (("ref_router.npz", fx), ("ref_closed_loop.npz", fc)):
+    written = []
+    if not ONLY or "router" in ONLY:
+        fx = {}
+        transport_cases(fx)
+        objective_cases(fx)
+        refine_cases(fx)
+        np.savez_compressed(os.path.join(HERE, "ref_router.npz"), **fx)
+        written.append(("ref_router.npz", fx))
+    if not ONLY or "closed_loop" in ONLY:
+        fc = {}
+        closed_loop_cases(fc)
+        np.savez_compressed(os.path.join(HERE, "ref_closed_loop.npz"), **fc)
+        written.append(("ref_closed_loop.npz", fc))
+    if not ONLY or "select" in ONLY:
+        fs = {}
+        select_cases(fs)
+        np.savez_compressed(os.path.join(HERE, "ref_select.npz"), **fs)
+        written.append(("ref_select.npz", fs))
+    for name, d in written:
         size = os.path.getsize(os.path.join(HERE, name))
         print(f"wrote {name}: {len(d)} arrays, {size / 1024:.0f} KiB")
 

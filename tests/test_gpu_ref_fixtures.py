@@ -2,12 +2,16 @@
 route_swap_kernel) and the device closed-loop allocator
 (rcsa_closed_loop_degrees) against fixtures written by the CAST reference's
 own FCPASMLocalCoordinateSwapRouter.refine (P/fc_pasm_swap_routing.py:616-1077)
-and compact_closed_loop_degrees (P/control_response_cwca_attention.py:1188-1363)
-(tests/golden/make_ref_golden.py)."""
+and compact_closed_loop_degrees (P/control_response_cwca_attention.py:1188-1363),
+and the device selection of the native layers (cast_amd.selector.taba_select:
+pooling, scores and top-k kernels) against the reference's own
+MatrixTrajectoryAdaptiveBudgetAttentionCompiler.select
+(P/qk_uncertainty_tangent_attention.py:988-1082) (tests/golden/make_ref_golden.py)."""
 import pytest
 import torch
 
-from tests._ref_fixtures import closed_loop_case, closed_loop_count, refine_case, refine_count
+from tests._ref_fixtures import (SELECT_CASES, closed_loop_case, closed_loop_count, refine_case,
+                                 refine_count, select_case)
 
 pytestmark = pytest.mark.gpu
 
@@ -57,3 +61,42 @@ def test_gpu_closed_loop_matches_reference(dev, ci):
     mem = p["memory"]
     assert torch.equal(got[:mem], torch.full((mem,), p["mean"], dtype=torch.long))
     assert torch.equal(got[mem:], c["degrees"].reshape(-1).long())
+
+
+@pytest.mark.parametrize("ci", range(len(SELECT_CASES)))
+def test_gpu_select_matches_reference(dev, ci):
+    """taba_select on a stand-in compiler holding the attributes the
+    reference's select reads: every row's selected prefix (rank order) and
+    count, and the report's budget fields, equal the reference's."""
+    from types import SimpleNamespace
+    from cast_amd.selector import taba_select
+    c = select_case(ci)
+    case = c["case"]
+    B, H = c["q"].shape[:2]
+    rows = torch.tensor(c["rows"], dtype=torch.long)
+    nb = rows.numel()
+    comp = SimpleNamespace(
+        _block_shape=tuple(case["block_shape"]), _num_blocks=nb, _degree=case["degree"],
+        _row_degrees=rows, _ray_motion=torch.linspace(0.1, 1.0, nb),
+        _first_order_motion=torch.linspace(0.2, 0.8, nb),
+        trajectory_complexity_kind="motion_magnitude")
+    comp._runtime_degrees = lambda q_blocks: comp._row_degrees
+    print(f"select fixture {ci}: B {B} H {H} blocks {nb} tile {case['block_shape']}", flush=True)
+    counts_in = torch.full((B, H, nb), case["degree"], dtype=torch.int32, device=dev)
+    sel, cnt, rep = taba_select(
+        comp, c["q"].to(dev), c["k"].to(dev),
+        geometry_indices=torch.zeros(B, H, nb, case["degree"], dtype=torch.int32, device=dev),
+        geometry_counts=counts_in, latent_hw=(case["height"], case["width"]),
+        block_shape=tuple(case["block_shape"]))
+    sel, cnt = sel.cpu(), cnt.cpu()
+    want = c["selected"].to(torch.int32)
+    assert torch.equal(cnt, c["counts"])
+    for b in range(B):
+        for h in range(H):
+            for r in range(nb):
+                n = int(rows[r])
+                assert torch.equal(sel[b, h, r, :n], want[b, h, r, :n]), (ci, b, h, r)
+    assert (rep.budget_min, rep.budget_max, rep.budget_total) == \
+        (int(rows.min()), int(rows.max()), int(rows.sum()))
+    assert abs(rep.mean_selected_qk_cosine - c["report"][0]) < 1e-5
+    assert rep.protected_local_edges == int(c["report"][1]) and rep.missing_local_edges == 0

@@ -1,7 +1,9 @@
-"""The oracle's router transport / objective / refine and closed-loop allocator
-against fixtures the CAST reference itself produced (tests/golden/make_ref_golden.py:
-P/fc_pasm_swap_routing.py:116-1077, P/control_response_cwca_attention.py:1123-1363),
-and the product's host-side transport operator against the same fixtures.
+"""The oracle's router transport / objective / refine, closed-loop allocator and
+native-layer selection (pooling, cosine scores, local stencil, top-k) against
+fixtures the CAST reference itself produced (tests/golden/make_ref_golden.py:
+P/fc_pasm_swap_routing.py:116-1077, P/control_response_cwca_attention.py:1123-1363,
+P/qk_uncertainty_tangent_attention.py:988-1082), and the product's host-side
+transport operator against the same fixtures.
 
 The GPU router and allocator are compared with these fixtures in
 tests/test_gpu_ref_fixtures.py.
@@ -10,9 +12,9 @@ import numpy as np
 import pytest
 import torch
 
-from tests._ref_fixtures import (closed_loop_case, closed_loop_count, objective_case,
-                                 oracle_operator, refine_case, refine_count, router_fixture,
-                                 transport_case)
+from tests._ref_fixtures import (SELECT_CASES, closed_loop_case, closed_loop_count,
+                                 objective_case, oracle_operator, refine_case, refine_count,
+                                 router_fixture, select_case, select_grid, transport_case)
 from oracle import rcsa_oracle as orc
 
 
@@ -137,3 +139,64 @@ def test_planted_closed_loop_mistake_is_caught():
     np.testing.assert_array_equal(
         orc.closed_loop_degrees(c["curvature"], c["frames"], **c["oracle_kw"])
         [c["params"]["memory"]:].numpy(), c["degrees"].reshape(-1).numpy())
+
+
+def _oracle_select(c, *, stencil_as_mask_only=False):
+    """The oracle's composition of the native select: visual tiles as the
+    compact layout of every frame, pool_blocks, block_scores, local_stencil,
+    select_topk in rank order at each row's budget.  The reference ranks a
+    local block by fl(score + 1e6) (a 0.0625 grid at 1e6), so the oracle is
+    given those values for the local columns, as the product does."""
+    case = c["case"]
+    q, k = c["q"], c["k"]
+    B, H = q.shape[:2]
+    idx, valid, _ = orc.compact_layout(range(case["T"]), 0, case["height"], case["width"],
+                                       case["block_shape"])
+    nb, bs = idx.shape
+    flat, vflat = idx.reshape(-1).clamp_min(0), valid.reshape(-1)
+
+    def pack(x):
+        return x[:, :, flat] * vflat[None, None, :, None]
+    qh, _, _ = orc.pool_blocks(pack(q), vflat, bs)
+    kh, _, _ = orc.pool_blocks(pack(k), vflat, bs)
+    score = orc.block_scores(qh, kh).reshape(B * H, nb, nb)
+    _, nh, nw = select_grid(case)
+    local = orc.local_stencil(nb, nh, nw)
+    ranking = score if stencil_as_mask_only else torch.where(local, (score + 1e6) - 1e6, score)
+    rows = c["rows"]
+    sel, cnt = orc.select_topk(ranking, torch.tensor(rows), forced=local, max_k=max(rows),
+                               order="rank")
+    return sel.reshape(B, H, nb, -1), cnt.reshape(B, H, nb), score
+
+
+@pytest.mark.parametrize("ci", range(len(SELECT_CASES)))
+def test_oracle_select_matches_reference(ci):
+    """Every row's selected prefix (its budget's worth, in rank order) and
+    count equal the reference's select()."""
+    c = select_case(ci)
+    sel, cnt, score = _oracle_select(c)
+    want = c["selected"]
+    assert torch.equal(cnt, c["counts"])
+    B, H, nb, _ = want.shape
+    for b in range(B):
+        for h in range(H):
+            for r in range(nb):
+                n = int(c["rows"][r])
+                assert torch.equal(sel[b, h, r, :n], want[b, h, r, :n].to(torch.int32)), \
+                    (ci, b, h, r)
+    rep = c["report"]
+    assert abs(float(score.double().mean()) - rep[0]) < 1e-6
+    assert [int(v) for v in rep[3:]] == [min(c["rows"]), max(c["rows"]), sum(c["rows"])]
+
+
+def test_select_fixtures_order_local_blocks_by_the_rounded_bonus():
+    """The reference orders the local blocks by fl(score + 1e6), not by the
+    exact score: ranking them by the exact score (the stencil only as a mask)
+    changes the rank order of some row, so the fixtures pin that detail."""
+    changed = False
+    for ci in range(len(SELECT_CASES)):
+        c = select_case(ci)
+        sel, _, _ = _oracle_select(c, stencil_as_mask_only=True)
+        want = c["selected"].to(torch.int32)
+        changed |= not torch.equal(sel[..., :want.shape[-1]], want)
+    assert changed
