@@ -5,7 +5,6 @@ Two calls in a row on split shapes, the second smaller, each bit-identical to
 the split entry point with a torch-allocated workspace; a split that would not
 fit the static scratch is refused with RCSA_ERR_SCRATCH before any launch.
 """
-import ctypes
 import math
 
 import pytest
