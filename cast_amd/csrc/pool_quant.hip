@@ -508,7 +508,11 @@ __device__ __forceinline__ void quant_tile(const PoolArgs& a, const float* kmean
         hi |= (static_cast<uint32_t>(quant_i8(v[j + 4] - m8[j + 4], inv)) & 0xffu) << (8 * j);
       }
     }
-    *reinterpret_cast<uint2*>(out + r * D + c * 8) = make_uint2(lo, hi);
+    // non-temporal: the int8 keys are read back only by the attention, after
+    // this pass, so they need not displace cached lines of the key passes
+    // (layer call at 3520 q x 38,720 kv, 24 heads: 0.502 against 0.509 ms)
+    const v2u packed = {lo, hi};
+    __builtin_nontemporal_store(packed, reinterpret_cast<v2u*>(out + r * D + c * 8));
   }
 }
 
