@@ -1,5 +1,6 @@
-"""Loading of the reference-produced router, closed-loop and select fixtures
-(tests/golden/ref_router.npz, ref_closed_loop.npz, ref_select.npz; written by
+"""Loading of the reference-produced router, closed-loop, select and
+apportionment fixtures (tests/golden/ref_router.npz, ref_closed_loop.npz,
+ref_select.npz, ref_apportion.npz; written by
 tests/golden/make_ref_golden.py) into the oracle's and the product's argument
 forms.  Shared by the CPU and GPU fixture tests (and by the script, for the
 select cases' seeded inputs)."""
@@ -199,3 +200,36 @@ def select_case(ci: int) -> dict:
     return {"case": case, "q": q, "k": k, "rows": fx[pre + "rows"].tolist(),
             "selected": _t(fx[pre + "selected"]), "counts": _t(fx[pre + "counts"]),
             "report": fx[pre + "report"].tolist()}
+
+
+# ---- largest-remainder apportionments (P/qk_uncertainty_tangent_attention.py:847-870,
+# 1239-1264) ----
+
+def apportion_cases() -> list:
+    """Every stored split: (name, weights [n] or [sections, n] float32, total,
+    reference result int64 of the same shape)."""
+    fx = router_fixture("apportion")
+    out = []
+    for key in sorted(k for k in fx if k.endswith("_w") and not k.startswith("motion")):
+        pre = key[:-2]
+        out.append((pre, _t(fx[key]), int(fx[pre + "_total"]), _t(fx[pre + "_out"])))
+    return out
+
+
+def motion_cases() -> list:
+    """(ray motion [n], degree, reference weights, reference row budgets)."""
+    fx = router_fixture("apportion")
+    return [(_t(fx[f"motion{i}_m"]), int(fx[f"motion{i}_degree"]), _t(fx[f"motion{i}_w"]),
+             _t(fx[f"motion{i}_out"])) for i in range(2)]
+
+
+def fp32_near_tie(weights: torch.Tensor, total: int, tol: float = 1e-5) -> bool:
+    """Whether two fractional parts of total * w / sum(w) (clamped weights, in
+    float64) lie within ``tol``: the rows where the fp32 rounding of the
+    quotient, not the exact quotient, decides the order."""
+    w = weights.double().clamp_min(0.0)
+    if not bool(w.sum() > 0):
+        w = torch.ones_like(w)
+    raw = w * total / w.sum()
+    fr = sorted((raw - raw.floor()).tolist(), reverse=True)
+    return any(abs(a - b) < tol for a, b in zip(fr, fr[1:]))

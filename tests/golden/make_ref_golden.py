@@ -1,12 +1,13 @@
 """Write reference-produced fixtures for the router transport / objective /
-refine and the closed-loop allocator: ``tests/golden/ref_router.npz`` and
-``tests/golden/ref_closed_loop.npz``.
+refine, the closed-loop allocator, the native select and the largest-remainder
+apportionments: ``tests/golden/ref_router.npz``, ``ref_closed_loop.npz``,
+``ref_select.npz`` and ``ref_apportion.npz``.
 
 Run in the build container only (the reference never travels to a GPU box):
 
     python tests/golden/make_ref_golden.py [/path/to/CAST]
 
-It imports two torch-only modules of the CAST reference and records, on small
+It imports three torch-only modules of the CAST reference and records, on small
 seeded CPU inputs, what these functions return:
 
 * ``FCPASMLocalCoordinateSwapRouter._apply_transport_maps`` and
@@ -38,7 +39,14 @@ Fixtures hold inputs and outputs only (numpy arrays, no pickles); the tests
 feed the inputs to the oracle and the product and compare with the outputs.
 P/ = src/interaction_accel/methods/proposed/.
 
-    python tests/golden/make_ref_golden.py [/path/to/CAST] [router|closed_loop|select ...]
+* ``MatrixTrajectoryAdaptiveBudgetAttentionCompiler._apportion`` and
+  ``._motion_weights`` (P/qk_uncertainty_tangent_attention.py:847-870) and
+  ``MatrixCurvatureTemperedUncertaintyAttentionCompiler._apportion_section_matrix``
+  (:1239-1264): the fp32 largest-remainder splits on random, zero, equal,
+  negative, decimal (near-tie) and peaked weights
+  (``tests/golden/ref_apportion.npz``, inputs stored beside the outputs).
+
+    python tests/golden/make_ref_golden.py [/path/to/CAST] [router|closed_loop|select|apportion ...]
 """
 from __future__ import annotations
 
@@ -50,8 +58,9 @@ import numpy as np
 import torch
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-_ARGS = [a for a in sys.argv[1:] if a not in ("router", "closed_loop", "select")]
-ONLY = [a for a in sys.argv[1:] if a in ("router", "closed_loop", "select")]
+GROUPS = ("router", "closed_loop", "select", "apportion")
+_ARGS = [a for a in sys.argv[1:] if a not in GROUPS]
+ONLY = [a for a in sys.argv[1:] if a in GROUPS]
 REF = _ARGS[0] if _ARGS else "/root/reference"
 sys.path.insert(0, os.path.join(REF, "src"))
 sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
@@ -318,6 +327,78 @@ def select_cases(fx):
                                        rep.budget_total], dtype=np.float64)
 
 
+def apportion_vectors():
+    """Weight vectors and totals for TABA._apportion: random weights of mixed
+    scales, all-zero and all-equal vectors, negative entries, decimal weights
+    whose fp32 fractional parts nearly tie, and peaked weights."""
+    g = torch.Generator().manual_seed(500)
+    cases = []
+    for n, total in ((7, 20), (28, 600), (300, 4096)):
+        scale = torch.tensor([1.0, 10.0, 1000.0])[torch.randint(0, 3, (n,), generator=g)]
+        cases.append((torch.rand(n, generator=g) * scale, total))
+    cases.append((torch.zeros(5), 7))
+    cases.append((torch.ones(9), 31))
+    w = torch.rand(12, generator=g)
+    w[::3] = -torch.rand(4, generator=g)
+    cases.append((w, 40))
+    cases.append((torch.tensor([0.1, 0.1, 0.1, 0.7]), 10))
+    cases.append((torch.tensor([0.1, 0.2, 0.3, 0.4, 0.1, 0.2, 0.3]), 13))
+    cases.append((torch.tensor([1.0 / 3.0] * 6 + [2.0 / 3.0] * 5), 17))
+    cases.append((torch.rand(853, generator=g) ** 4, 853 * 5))
+    # decimal weights whose fp32 quotients tie (or swap) fractional parts that
+    # differ in exact arithmetic on the same fp32 inputs
+    cases.append((torch.tensor([0.2, 0.7, 0.3]), 30))
+    cases.append((torch.tensor([1.0, 4.2, 0.8, 0.3]), 9))
+    cases.append((torch.tensor([0.6, 1.35, 2.4, 0.45, 7.2, 0.2, 1.8]), 36))
+    return [(w.float(), t) for w, t in cases]
+
+
+def apportion_matrices():
+    """Section matrices and per-section totals for
+    MatrixCurvatureTemperedUncertaintyAttentionCompiler._apportion_section_matrix:
+    random rows, a zero row, an all-equal row, a row with negatives, a decimal
+    row, and decimal rows whose fp32 fractional parts order differently from
+    exact arithmetic."""
+    g = torch.Generator().manual_seed(501)
+    out = []
+    for S, n, total in ((6, 7, 23), (5, 40, 300), (4, 260, 1500)):
+        w = torch.rand(S, n, generator=g) * torch.tensor([1.0, 10.0, 1000.0])[
+            torch.randint(0, 3, (S, n), generator=g)]
+        w[1] = 0.0
+        w[2] = 1.0
+        w[3, ::2] = -1.0
+        if S > 4:
+            w[4] = torch.tensor([0.1, 0.2, 0.3, 0.4])[torch.arange(n) % 4]
+        out.append((w.float(), total))
+    out.append((torch.tensor([[3.6, 0.05, 0.45, 4.9, 0.6, 1.05, 0.6],
+                              [3.6, 4.9, 0.9, 1.4, 1.2, 1.8, 2.7],
+                              [0.3, 0.6, 6.3, 1.4, 6.3, 1.5, 8.1]]), 30))
+    return out
+
+
+def apportion_cases(fx):
+    """The reference's largest-remainder apportionments: the 1-D TABA form,
+    the row-wise section form, and TABA's motion weights feeding it."""
+    TABA = Q.MatrixTrajectoryAdaptiveBudgetAttentionCompiler
+    SECT = Q.MatrixCurvatureTemperedUncertaintyAttentionCompiler
+    for i, (w, total) in enumerate(apportion_vectors()):
+        fx[f"vec{i}_w"] = w.numpy()
+        fx[f"vec{i}_total"] = np.array(total, dtype=np.int64)
+        fx[f"vec{i}_out"] = TABA._apportion(w.clone(), total).numpy()
+    for i, (w, total) in enumerate(apportion_matrices()):
+        fx[f"mat{i}_w"] = w.numpy()
+        fx[f"mat{i}_total"] = np.array(total, dtype=np.int64)
+        fx[f"mat{i}_out"] = SECT._apportion_section_matrix(w.clone(), total).numpy()
+    g = torch.Generator().manual_seed(502)
+    for i, (n, degree) in enumerate(((30, 7), (330, 21))):
+        motion = torch.rand(n, generator=g) ** 2
+        weights = TABA._motion_weights(motion)
+        fx[f"motion{i}_m"] = motion.numpy()
+        fx[f"motion{i}_degree"] = np.array(degree, dtype=np.int64)
+        fx[f"motion{i}_w"] = weights.numpy()
+        fx[f"motion{i}_out"] = TABA._apportion(weights, n * degree).numpy()
+
+
 def main():
     torch.manual_seed(0)
     written = []
@@ -338,6 +419,11 @@ def main():
         select_cases(fs)
         np.savez_compressed(os.path.join(HERE, "ref_select.npz"), **fs)
         written.append(("ref_select.npz", fs))
+    if not ONLY or "apportion" in ONLY:
+        fa = {}
+        apportion_cases(fa)
+        np.savez_compressed(os.path.join(HERE, "ref_apportion.npz"), **fa)
+        written.append(("ref_apportion.npz", fa))
     for name, d in written:
         size = os.path.getsize(os.path.join(HERE, name))
         print(f"wrote {name}: {len(d)} arrays, {size / 1024:.0f} KiB")

@@ -6,12 +6,15 @@ and compact_closed_loop_degrees (P/control_response_cwca_attention.py:1188-1363)
 and the device selection of the native layers (cast_amd.selector.taba_select:
 pooling, scores and top-k kernels) against the reference's own
 MatrixTrajectoryAdaptiveBudgetAttentionCompiler.select
-(P/qk_uncertainty_tangent_attention.py:988-1082) (tests/golden/make_ref_golden.py)."""
+(P/qk_uncertainty_tangent_attention.py:988-1082), and the device per-row
+budgets (rcsa_row_budgets) against its _apportion and _apportion_section_matrix
+(:847-865, 1239-1264) (tests/golden/make_ref_golden.py)."""
 import pytest
 import torch
 
-from tests._ref_fixtures import (SELECT_CASES, closed_loop_case, closed_loop_count, refine_case,
-                                 refine_count, select_case)
+from tests._ref_fixtures import (SELECT_CASES, apportion_cases, closed_loop_case,
+                                 closed_loop_count, fp32_near_tie, refine_case, refine_count,
+                                 select_case)
 
 pytestmark = pytest.mark.gpu
 
@@ -100,3 +103,25 @@ def test_gpu_select_matches_reference(dev, ci):
         (int(rows.min()), int(rows.max()), int(rows.sum()))
     assert abs(rep.mean_selected_qk_cosine - c["report"][0]) < 1e-5
     assert rep.protected_local_edges == int(c["report"][1]) and rep.missing_local_edges == 0
+
+
+def test_gpu_row_budgets_match_reference(dev):
+    """Every stored split, one section per row: bit for bit, except that a row
+    whose fractional parts tie within 1e-5 may move one edge (the device sums
+    the weights in a fixed tree order, the reference in torch's; the quotients
+    can then round to the other side of the tie)."""
+    from cast_amd import ops
+    exact = 0
+    for name, w, total, want in apportion_cases():
+        rows = (w if w.ndim == 2 else w[None]).contiguous()
+        wants = want if want.ndim == 2 else want[None]
+        print(f"row budgets fixture {name}: {tuple(rows.shape)} total {total}", flush=True)
+        got = ops.row_budgets(rows.to(dev), total).cpu().long()
+        for r in range(rows.shape[0]):
+            assert int(got[r].sum()) == total, (name, r)
+            if torch.equal(got[r], wants[r]):
+                exact += 1
+                continue
+            assert fp32_near_tie(rows[r], total), (name, r)
+            assert int((got[r] - wants[r]).abs().max()) <= 1, (name, r)
+    assert exact >= 20

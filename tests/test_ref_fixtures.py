@@ -1,9 +1,11 @@
-"""The oracle's router transport / objective / refine, closed-loop allocator and
-native-layer selection (pooling, cosine scores, local stencil, top-k) against
-fixtures the CAST reference itself produced (tests/golden/make_ref_golden.py:
-P/fc_pasm_swap_routing.py:116-1077, P/control_response_cwca_attention.py:1123-1363,
-P/qk_uncertainty_tangent_attention.py:988-1082), and the product's host-side
-transport operator against the same fixtures.
+"""The oracle's router transport / objective / refine, closed-loop allocator,
+native-layer selection (pooling, cosine scores, local stencil, top-k) and
+largest-remainder apportionments against fixtures the CAST reference itself
+produced (tests/golden/make_ref_golden.py: P/fc_pasm_swap_routing.py:116-1077,
+P/control_response_cwca_attention.py:1123-1363,
+P/qk_uncertainty_tangent_attention.py:847-870, 988-1082, 1239-1264), and the
+product's host-side transport operator and budget splits against the same
+fixtures.
 
 The GPU router and allocator are compared with these fixtures in
 tests/test_gpu_ref_fixtures.py.
@@ -12,9 +14,10 @@ import numpy as np
 import pytest
 import torch
 
-from tests._ref_fixtures import (SELECT_CASES, closed_loop_case, closed_loop_count,
-                                 objective_case, oracle_operator, refine_case, refine_count,
-                                 router_fixture, select_case, select_grid, transport_case)
+from tests._ref_fixtures import (SELECT_CASES, apportion_cases, closed_loop_case,
+                                 closed_loop_count, fp32_near_tie, motion_cases, objective_case,
+                                 oracle_operator, refine_case, refine_count, router_fixture,
+                                 select_case, select_grid, transport_case)
 from oracle import rcsa_oracle as orc
 
 
@@ -200,3 +203,54 @@ def test_select_fixtures_order_local_blocks_by_the_rounded_bonus():
         want = c["selected"].to(torch.int32)
         changed |= not torch.equal(sel[..., :want.shape[-1]], want)
     assert changed
+
+
+# ---- largest-remainder apportionments ----
+
+def test_fp32_apportion_matches_reference():
+    """orc.apportion_section_matrix_f32 (the reference's fp32 arithmetic) equals
+    the reference's _apportion and _apportion_section_matrix on every stored
+    split, the fp32 near-tie cases included."""
+    cases = apportion_cases()
+    assert len(cases) >= 17
+    for name, w, total, want in cases:
+        mat = w if w.ndim == 2 else w[None]
+        got = orc.apportion_section_matrix_f32(mat, total).reshape(want.shape)
+        assert torch.equal(got, want), name
+        assert bool((want.sum(dim=-1) == total).all()), name
+
+
+def test_exact_apportion_differs_from_reference_only_at_fp32_ties():
+    """The exact-rational restatement (orc.apportion) equals the reference
+    except on rows whose fractional parts tie within 1e-5, where fp32 rounding
+    decides; the fixtures hold such rows (decimal weights), so the difference
+    is real and confined to them."""
+    differing = 0
+    for name, w, total, want in apportion_cases():
+        rows = w if w.ndim == 2 else w[None]
+        wants = want if want.ndim == 2 else want[None]
+        for r in range(rows.shape[0]):
+            got = orc.apportion(rows[r].tolist(), total)
+            if got != wants[r].tolist():
+                differing += 1
+                assert fp32_near_tie(rows[r], total), (name, r)
+                assert sum(got) == total
+                assert max(abs(a - b) for a, b in zip(got, wants[r].tolist())) <= 1
+    assert differing >= 4
+
+
+def test_host_budget_splits_match_reference():
+    """cast_amd.budget.apportion / apportion_section_matrix and the motion
+    row budgets (1 + motion / (mean + eps), then _apportion of n * degree)
+    equal the reference bit for bit."""
+    from cast_amd import budget
+    for name, w, total, want in apportion_cases():
+        got = (budget.apportion_section_matrix(w, total) if w.ndim == 2
+               else budget.apportion(w, total))
+        assert torch.equal(got, want), name
+    for motion, degree, w_ref, rows_ref in motion_cases():
+        n = motion.numel()
+        eps = torch.finfo(torch.float32).eps
+        assert torch.equal(1.0 + motion / (motion.mean() + eps), w_ref)
+        rows = budget.motion_row_degrees(motion, degree, torch.zeros(n, 1, dtype=torch.bool))
+        assert torch.equal(rows, rows_ref)
