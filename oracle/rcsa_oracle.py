@@ -917,7 +917,9 @@ def fc_pasm_refine(score: torch.Tensor, pooled_value: torch.Tensor, selected: to
     index), the omission proxy of each candidate, and up to num_swap_rounds
     rounds that each apply the single best (remove, add) exchange over all
     current rows when it lowers the objective by more than swap_eps
-    (:843-977), with the same-bank rule when configured.  ``config`` carries the
+    (:843-977), with the same-bank rule when configured, and the checks on the
+    final route that raise (:980-1033: same-bank memory counts, duplicate keys, a
+    dropped local-stencil edge, a higher objective).  ``config`` carries the
     FCPASMSwapRoutingConfig fields; ``operator(pair, exponent)`` gives the FC
     transport operator of a pair (None: identity).  Returns (selected, record).
     """
@@ -1043,6 +1045,10 @@ def fc_pasm_refine(score: torch.Tensor, pooled_value: torch.Tensor, selected: to
         torch.triu(torch.ones(K, K, dtype=torch.bool), diagonal=1)
     if bool(dup.any()):
         raise RuntimeError("FC-PASM routing emitted duplicate keys")
+    kept_local = torch.gather(local[None, None].expand(*sel.shape[:2], -1, -1), -1,
+                              sel.clamp_min(0)) & v
+    if int(kept_local.sum()) != int(local.sum()) * sel.shape[0] * sel.shape[1]:
+        raise RuntimeError("FC-PASM routing removed a protected local edge")
     obj_after = route_objective_value(cur_err, **okw)
     if bool(obj_after > obj_before + 1e-5 * obj_before.abs().clamp_min(1.0)):
         raise RuntimeError("FC-PASM swap increased its refinement objective")

@@ -168,3 +168,28 @@ def test_refine_with_published_transport(dev):
     assert torch.equal(got.cpu(), want)
     assert abs(float(rec["objective_after"]) - rec_w["objective_after"]) <= \
         1e-4 * abs(rec_w["objective_after"])
+
+
+def test_refine_refuses_invalid_routes(dev):
+    """The device router raises the reference's errors on routes that fail its
+    final checks (P/fc_pasm_swap_routing.py:980-1033), as the oracle does: a row
+    that drops its local stencil, a row that lists a key twice."""
+    from cast_amd.router import FCPASMSwapRouter
+    score, pv, sel, cnt, local = _case(2)
+    cfg = _cfg(num_swap_rounds=1)
+    kw = dict(memory_blocks=MEM, spatial_shape=HW, exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, layer_index=22, transport=None)
+    dropped = cnt.clone()
+    dropped[0, 1, MEM + 4] = 0                 # a current row keeps nothing
+    twice = sel.clone()
+    twice[0, 0, 3, 1] = twice[0, 0, 3, 0]      # a memory row lists its first key twice
+    router = FCPASMSwapRouter(cfg)
+    for s, c, msg in ((sel, dropped, "removed a protected local edge"),
+                      (twice, cnt, "duplicate keys")):
+        print(f"refine refuses: {msg}", flush=True)
+        with pytest.raises(RuntimeError, match=msg):
+            orc.fc_pasm_refine(score, pv, s, c, local, config=cfg, **kw)
+        with pytest.raises(RuntimeError, match=msg):
+            router.refine(score=score.to(dev), pooled_value=pv.to(dev), selected=s.to(dev),
+                          counts=c.to(dev), local=local.to(dev), **kw)
+        torch.cuda.synchronize()

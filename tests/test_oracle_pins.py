@@ -727,6 +727,26 @@ def test_route_fallbacks_are_identity():
         assert rec["swap_count"] == 0 and rec["status"] == "independent_topk_fallback"
 
 
+def test_refine_refuses_invalid_routes():
+    """The checks on the final route (P/fc_pasm_swap_routing.py:980-1033): a
+    route that does not hold a row's local stencil, or holds a key twice,
+    raises the reference's error."""
+    score, pv, sel, cnt, local = _route_case(1)
+    kw = dict(memory_blocks=6, spatial_shape=(2, 3), exact_current_frames=(0, 6),
+              temporal_group_size=4, current_boundary=8, layer_index=0, transport=None)
+    cfg = _route_cfg()
+    out, rec = orc.fc_pasm_refine(score, pv, sel, cnt, local, config=cfg, **kw)
+    assert rec["status"] == "refined"
+    dropped = cnt.clone()
+    dropped[0, 1, 9] = 0                   # row 9 keeps nothing, not even itself
+    with pytest.raises(RuntimeError, match="removed a protected local edge"):
+        orc.fc_pasm_refine(score, pv, sel, dropped, local, config=cfg, **kw)
+    twice = sel.clone()
+    twice[0, 0, 2, 1] = twice[0, 0, 2, 0]  # memory row 2 lists its first key twice
+    with pytest.raises(RuntimeError, match="duplicate keys"):
+        orc.fc_pasm_refine(score, pv, twice, cnt, local, config=cfg, **kw)
+
+
 def test_omission_proxy_fp64_loops():
     g = torch.Generator().manual_seed(3)
     B, H, Q, K, D, L, G = 1, 2, 5, 9, 32, 4, 16
