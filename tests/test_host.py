@@ -1,6 +1,7 @@
 """Host-side tests that need no GPU: the C-ABI library loads and exports what
-``include/rcsa.h`` declares, the Python wrappers fail loudly off-device, and
-the synthetic workloads have the shapes and budgets of the benchmark cases."""
+``include/rcsa.h`` declares, the Python wrappers fail loudly off-device, the
+synthetic workloads have the shapes and budgets of the benchmark cases, and
+bench.py refuses more than one GPU."""
 import re
 from pathlib import Path
 
@@ -165,3 +166,14 @@ def test_step_sweep_plan_and_layer_view():
         assert int(w.q_valid.sum()) == lq and w.n_qblocks == -(-lq // 128)
         assert int(w.k_valid[w.n_hist_blocks * 128:].sum()) == lq
         assert torch.all(w.q[:, :, lq:] == 0)
+
+
+def test_bench_runs_on_one_gpu_only():
+    """bench.py --gpus N with N above 1 stops before touching a device, with a
+    message that says why (the path shards heads with no exchange)."""
+    import subprocess
+    import sys
+    res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120, cwd=ROOT)
+    assert res.returncode == 2
+    assert "one GPU" in res.stderr + res.stdout and "--gpus 2" in res.stderr + res.stdout
