@@ -592,6 +592,9 @@ int rcsa_route_check(const int32_t* base, const int32_t* selected, const int32_t
  * [N][K] (both 16-byte aligned), w_scale fp32 [N] (16-byte aligned), bias bf16
  * [N] or NULL (then out = bf16(float(acc) * x_scale * w_scale)); out bf16 with
  * row stride ldo (8-byte aligned).  N a multiple of 256, K a multiple of 128.
+ * The launch is persistent (one workgroup per compute unit, each with a fixed
+ * share of the tiles): it expects the device to itself, and beside other
+ * kernels it stays correct but runs as slowly as its latest workgroup.
  */
 int rcsa_quantize_rows_int8(const void* x, int dtype, int64_t M, int64_t C, int64_t ldx,
                             int8_t* q, float* scale, hipStream_t stream);
