@@ -81,20 +81,6 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
-// Map a hardware workgroup id to a logical work item so that consecutive
-// work items land on the same XCD (and share its L2).  The grid must be
-// launched with kNumXcd * per_xcd workgroups; ids mapping past n_work
-// return -1 and must exit.
-__device__ __forceinline__ int64_t xcd_remap(int64_t wg, int64_t n_work) {
-  int64_t per_xcd = (n_work + kNumXcd - 1) / kNumXcd;
-  int64_t work = (wg % kNumXcd) * per_xcd + wg / kNumXcd;
-  return work < n_work ? work : -1;
-}
-inline int64_t xcd_grid(int64_t n_work) {
-  int64_t per_xcd = (n_work + kNumXcd - 1) / kNumXcd;
-  return per_xcd * kNumXcd;
-}
-
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? RCSA_OK : RCSA_ERR_LAUNCH;
