@@ -315,8 +315,8 @@ __device__ __forceinline__ void small_tile(const LinearArgs& a, int64_t m0, int6
 // XCD-local big tile `work` -> its origin.  Consecutive work items of an XCD
 // walk groups of kGroupM token blocks for one channel block, then the next,
 // so the 32 workgroups of an XCD share 4 token blocks and 8 weight blocks in
-// its L2 (at 38,720 x 3072 x 3072: 0.458 ms with 4 blocks per group; 2, 8 and
-// 16: 0.467, 0.462 and 0.469 ms, measured on an earlier form of the kernel).
+// its L2 (at 38,720 x 3072 x 3072, interleaved on one box: 0.398-0.403 ms with
+// 4 blocks per group; 2, 6 and 8: 0.407-0.414, 0.399-0.410 and 0.404-0.409 ms).
 __device__ __forceinline__ bool big_tile_of(const LinearArgs& a, int64_t work, int64_t* m0,
                                             int64_t* n0) {
   constexpr int64_t kGroupM = 4;
